@@ -1,0 +1,229 @@
+"""Benchmark of the int8 projection + paged-attention decode path on one MI355X.
+
+Default workload: TinyLlama-1.1B-shaped int8 decode at batch 1,
+random-init weights N(0, 0.02) quantized per row (lm_head int8 too), a 512-token random
+prompt prefilled on the GPU, then greedy decode steps. A "step" is one decode step of the
+batch (one pia_model_decode call: every layer, the LM head, argmax, token fed back).
+
+Also reported (same line): the batch-32 paged decode of configs[2] (contexts U[128, 2048],
+blocks assigned by a random permutation of the pool), the dominant kernel's roofline from
+HIP events on the library's stream, and the CPU baseline (the oracle's restatement of the
+reference's rayon + AVX2 path) timed on a bounded sample on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-b32] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "paged-infer_amd"))
+import pia  # noqa: E402
+
+METRIC = "int8 decode tok/s (B=1,32) + int8 GEMV HBM GB/s as % of ~8 TB/s peak"
+HBM_PEAK_GBS = 8000.0
+SEED = 2024
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def host_cores() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, int(os.environ.get("OMP_NUM_THREADS", n))))
+
+
+def decode_loop(model, toks, positions, tables, steps, bs, mgr=None):
+    """Greedy decode `steps` steps; returns the final tokens. Blocks are pre-mapped."""
+    toks = list(toks)
+    positions = list(positions)
+    for _ in range(steps):
+        _, am = model.decode(toks, positions, tables, want_logits=False)
+        toks = am.tolist()
+        positions = [p + 1 for p in positions]
+    return toks, positions
+
+
+def run_b1(ctx, cfg, weights, steps, warmup, prompt_len=512):
+    bs = 16
+    total_tokens = prompt_len + warmup + 2 * steps + 8
+    nb = (total_tokens + bs - 1) // bs
+    table = list(range(nb))
+    model = pia.Model(ctx, cfg, weights)
+    model.kv_alloc(nb, bs)
+    prompt = np.random.default_rng(SEED).integers(0, cfg.vocab, prompt_len).tolist()
+    t0 = time.perf_counter()
+    _, tok = model.prefill(prompt, 0, table, want_logits=False)
+    ctx.sync()
+    prefill_s = time.perf_counter() - t0
+    toks, pos = decode_loop(model, [tok], [prompt_len], [table], warmup, bs)
+    # Timed region: K decode steps, per-kernel HIP events recorded on the library stream.
+    model.profile(True)
+    gemv_ms = attn_ms = other_ms = 0.0
+    gemv_bytes = attn_bytes = 0
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        _, am = model.decode(toks, pos, [table], want_logits=False)
+        ms, by = model.profile_get()
+        gemv_ms += ms[0]
+        attn_ms += ms[1]
+        other_ms += ms[2]
+        gemv_bytes += int(by[0])
+        attn_bytes += int(by[1])
+        toks = am.tolist()
+        pos = [p + 1 for p in pos]
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    model.profile(False)
+    kv_state = model.kv_download() if os.environ.get("BENCH_CPU", "1") == "1" else None
+    res = dict(tok_s=steps / elapsed, ms_per_step=1e3 * elapsed / steps, prefill_tok_s=prompt_len / prefill_s,
+               gemv_ms=gemv_ms / steps, attn_ms=attn_ms / steps, other_ms=other_ms / steps,
+               gemv_bytes=gemv_bytes / steps, attn_bytes=attn_bytes / steps, last_tok=toks[0], last_pos=pos[0],
+               table=table, nb=nb, weight_bytes=model.weight_bytes())
+    model.close()
+    return res, kv_state
+
+
+def run_b32(ctx, cfg, weights, steps, warmup, batch=32):
+    bs = 16
+    rng = np.random.default_rng(SEED + 32)
+    ctxs = rng.integers(128, 2049, batch)
+    need = [(int(c) + warmup + steps + 2 + bs - 1) // bs for c in ctxs]
+    nb = sum(need)
+    perm = rng.permutation(nb).tolist()
+    tables, k = [], 0
+    for n in need:
+        tables.append(perm[k:k + n])
+        k += n
+    model = pia.Model(ctx, cfg, weights)
+    model.kv_alloc(nb, bs)
+    first = []
+    t0 = time.perf_counter()
+    for b in range(batch):
+        prompt = rng.integers(0, cfg.vocab, int(ctxs[b])).tolist()
+        _, t = model.prefill(prompt, 0, tables[b], want_logits=False)
+        first.append(t)
+    ctx.sync()
+    prefill_s = time.perf_counter() - t0
+    toks, pos = decode_loop(model, first, [int(c) for c in ctxs], tables, warmup, bs)
+    model.profile(True)
+    gemv_ms = attn_ms = 0.0
+    gemv_bytes = attn_bytes = 0
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        _, am = model.decode(toks, pos, tables, want_logits=False)
+        ms, by = model.profile_get()
+        gemv_ms += ms[0]
+        attn_ms += ms[1]
+        gemv_bytes += int(by[0])
+        attn_bytes += int(by[1])
+        toks = am.tolist()
+        pos = [p + 1 for p in pos]
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    model.close()
+    return dict(tok_s=batch * steps / elapsed, ms_per_step=1e3 * elapsed / steps,
+                prefill_tok_s=float(np.sum(ctxs)) / prefill_s, mean_ctx=float(np.mean(ctxs)),
+                gemv_gbs=(gemv_bytes / 1e9) / (gemv_ms / 1e3) if gemv_ms else None,
+                attn_gbs=(attn_bytes / 1e9) / (attn_ms / 1e3) if attn_ms else None,
+                gemv_ms=gemv_ms / steps, attn_ms=attn_ms / steps)
+
+
+def cpu_baseline(cfg, weights, b1, kv_state, budget_s=15.0):
+    """The oracle (C++ restatement of the reference's rayon + AVX2 path) decoding at batch 1
+    from the GPU run's KV state, on this host's cores, for a bounded number of steps."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as orc
+    cores = host_cores()
+    orc.set_threads(cores)
+    om = orc.OracleModel(cfg, weights)
+    tok, pos, table, nb = b1["last_tok"], b1["last_pos"], b1["table"], b1["nb"]
+    kv = kv_state
+    t0 = time.perf_counter()
+    lc = om.decode([tok], [pos], [table], kv, nb, 16)
+    one = time.perf_counter() - t0
+    n = int(max(2, min(200, budget_s / max(one, 1e-3))))
+    tok = orc.argmax(lc[0])
+    pos += 1
+    t0 = time.perf_counter()
+    for _ in range(n):
+        lc = om.decode([tok], [pos], [table], kv, nb, 16)
+        tok = orc.argmax(lc[0])
+        pos += 1
+    el = time.perf_counter() - t0
+    return {"value": n / el, "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{n} greedy decode steps at batch 1 (TinyLlama shape, int8 incl. lm_head) from the GPU "
+                      f"run's KV state at position {b1['last_pos']}, oracle/ref_cpu.cpp with {cores} threads, "
+                      f"avx2={bool(orc.lib().orc_have_avx2())}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-b32", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the int8 decode path is built and measured on a single MI355X; "
+              "multi-GPU sharding is design-only (DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if args.no_cpu:
+        os.environ["BENCH_CPU"] = "0"
+
+    cfg = pia.TINYLLAMA
+    log("building synthetic TinyLlama int8 weights")
+    weights = pia.synth_weights(cfg, seed=SEED)
+    ctx = pia.Context(0)
+    log("B=1 decode")
+    b1, kv_state = run_b1(ctx, cfg, weights, args.steps, args.warmup)
+    gemv_gbs = (b1["gemv_bytes"] / 1e9) / (b1["gemv_ms"] / 1e3)
+    out = {
+        "metric": METRIC,
+        "value": round(b1["tok_s"], 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(b1["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8w-f32",
+        "data": "synthetic (seeded N(0,0.02) weights -> per-row int8; uniform random prompt)",
+        "config": {"workload": "tinyllama-1.1b-shape int8 decode, batch 1, 512-token prompt (configs[1])",
+                   "batch": 1, "prompt_tokens": 512, "block_size": 16, "lm_head": "int8",
+                   "weight_bytes": b1["weight_bytes"], "prefill_tok_s": round(b1["prefill_tok_s"], 1),
+                   "gemv_ms_per_step": round(b1["gemv_ms"], 4), "attention_ms_per_step": round(b1["attn_ms"], 4),
+                   "other_ms_per_step": round(b1["other_ms"], 4)},
+        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_gemv (all int8 projections + lm_head of a step, aggregated)"},
+    }
+    if not args.no_b32:
+        log("B=32 paged decode")
+        b32 = run_b32(ctx, cfg, weights, max(5, args.steps // 4), max(2, args.warmup // 2))
+        out["b32"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in b32.items()}
+    if not args.no_cpu:
+        log("CPU baseline")
+        out["cpu_baseline"] = cpu_baseline(cfg, weights, b1, kv_state)
+    ctx.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

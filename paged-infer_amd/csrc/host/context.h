@@ -1,0 +1,59 @@
+// Host-side state shared by the C ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "paged_infer_amd.h"
+
+struct pia_context {
+  int device = 0;
+  int num_cus = 0;
+  hipStream_t stream = nullptr;
+};
+
+namespace pia {
+
+// Grow-only device allocation.
+struct DeviceBuffer {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  DeviceBuffer() = default;
+  DeviceBuffer(const DeviceBuffer&) = delete;
+  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+  DeviceBuffer(DeviceBuffer&& o) noexcept : ptr(o.ptr), bytes(o.bytes) { o.ptr = nullptr, o.bytes = 0; }
+  DeviceBuffer& operator=(DeviceBuffer&& o) noexcept {
+    if (this != &o) {
+      release();
+      ptr = o.ptr, bytes = o.bytes;
+      o.ptr = nullptr, o.bytes = 0;
+    }
+    return *this;
+  }
+  ~DeviceBuffer();
+  void ensure(size_t need);
+  void release();
+  template <typename T>
+  T* as() const {
+    return static_cast<T*>(ptr);
+  }
+};
+
+// Grow-only pinned host allocation (hipHostMalloc).
+struct PinnedBuffer {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  PinnedBuffer() = default;
+  PinnedBuffer(const PinnedBuffer&) = delete;
+  PinnedBuffer& operator=(const PinnedBuffer&) = delete;
+  ~PinnedBuffer();
+  void ensure(size_t need);
+};
+
+hipStream_t stream_of(pia_context* ctx, void* stream);
+void check_layout(const pia_kv_layout* L);
+void quantize_rows_host(const float* w, int64_t rows, int64_t cols, int8_t* q, float* scales);
+
+}  // namespace pia

@@ -1,0 +1,549 @@
+// Device-resident Llama weights + paged KV cache, and the batched forward pass
+// (LlamaWeights::run_layers_batch / decode_batch_into / prefill_batched, src/model.rs:968-1255).
+//
+// Weight layout in HBM: q/k/v rows concatenated into one [hidden + 2*kv_dim][ld] matrix and
+// gate/up rows into one [2*inter][ld] matrix, so a decode layer streams its weights in four
+// launches; rows are padded to 16 bytes (int8) so every lane issues aligned 128-bit loads.
+// Activations are [batch][ld] f32 with ld a multiple of 16 floats.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "../common.h"
+#include "../kernels.h"
+#include "context.h"
+
+namespace pia {
+namespace {
+
+inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+struct Proj {
+  int kind = -1;  // -1 unset, 0 f32, 1 int8
+  int64_t rows = 0, cols = 0, ld = 0;
+  DeviceBuffer w, s;
+  uint32_t filled = 0;  // bitmask of filled sub-matrices
+};
+
+struct Layer {
+  DeviceBuffer attn_norm, ffn_norm;
+  Proj qkv, o, gu, down;
+};
+
+// Per-launch timing, by kernel class.
+struct Prof {
+  bool on = false;
+  struct Rec {
+    int cls;
+    int64_t bytes;
+    hipEvent_t a, b;
+  };
+  std::vector<hipEvent_t> pool;
+  std::vector<Rec> recs;
+  size_t used = 0;
+  double ms[3] = {0, 0, 0};
+  int64_t bytes[3] = {0, 0, 0};
+
+  hipEvent_t ev() {
+    if (used == pool.size()) {
+      hipEvent_t e;
+      PIA_HIP(hipEventCreate(&e));
+      pool.push_back(e);
+    }
+    return pool[used++];
+  }
+  void reset() {
+    recs.clear();
+    used = 0;
+  }
+  ~Prof() {
+    for (auto e : pool) (void)hipEventDestroy(e);
+  }
+};
+
+}  // namespace
+}  // namespace pia
+
+using namespace pia;
+
+struct pia_model {
+  pia_context* ctx = nullptr;
+  pia_model_config cfg{};
+  int64_t hd = 0, kvd = 0, qkv_rows = 0;
+  int64_t ld_h = 0, ld_qkv = 0, ld_gu = 0, ld_i = 0, ld_v = 0;
+  DeviceBuffer embed, final_norm;
+  bool embed_set = false, final_norm_set = false;
+  std::vector<Layer> layers;
+  Proj lm_head;
+
+  DeviceBuffer kv;
+  pia_kv_layout layout{};
+
+  DeviceBuffer rope_cos, rope_sin;
+  int64_t rope_len = 0;
+
+  int64_t cap = 0;  // rows of activation scratch
+  DeviceBuffer x, xb, qkv, attn, gu, h, logits, amax, attn_work, step;
+  PinnedBuffer pin;
+  Prof prof;
+
+  hipStream_t st() const { return ctx->stream; }
+
+  void begin(int cls, int64_t bytes, hipEvent_t* b) {
+    if (!prof.on) return;
+    hipEvent_t a = prof.ev();
+    *b = prof.ev();
+    PIA_HIP(hipEventRecord(a, st()));
+    prof.recs.push_back({cls, bytes, a, *b});
+  }
+  void end(hipEvent_t b) {
+    if (prof.on) PIA_HIP(hipEventRecord(b, st()));
+  }
+
+  void ensure_cap(int64_t rows) {
+    if (rows <= cap) return;
+    const int64_t c = std::max<int64_t>(rows, 8);
+    x.ensure(c * ld_h * 4);
+    xb.ensure(c * ld_h * 4);
+    qkv.ensure(c * ld_qkv * 4);
+    attn.ensure(c * ld_h * 4);
+    gu.ensure(c * ld_gu * 4);
+    h.ensure(c * ld_i * 4);
+    amax.ensure(c * 4);
+    cap = c;
+  }
+
+  void ensure_rope(int64_t max_pos) {
+    if (max_pos < rope_len) return;
+    int64_t n = std::max<int64_t>(1024, rope_len);
+    while (n <= max_pos) n *= 2;
+    const int64_t half = hd / 2;
+    std::vector<float> c(n * half), s(n * half);
+    // rope_table (src/math.rs:331-341), with the same libm calls as the reference's f32 methods.
+    for (int64_t j = 0; j < half; ++j) {
+      const float freq = 1.0f / powf(cfg.rope_theta, static_cast<float>(2 * j) / static_cast<float>(hd));
+      for (int64_t p = 0; p < n; ++p) {
+        const float a = static_cast<float>(p) * freq;
+        c[p * half + j] = cosf(a);
+        s[p * half + j] = sinf(a);
+      }
+    }
+    PIA_HIP(hipStreamSynchronize(st()));
+    rope_cos.release();
+    rope_sin.release();
+    rope_cos.ensure(c.size() * 4);
+    rope_sin.ensure(s.size() * 4);
+    PIA_HIP(hipMemcpy(rope_cos.ptr, c.data(), c.size() * 4, hipMemcpyHostToDevice));
+    PIA_HIP(hipMemcpy(rope_sin.ptr, s.data(), s.size() * 4, hipMemcpyHostToDevice));
+    rope_len = n;
+  }
+
+  int64_t proj_bytes(const Proj& p, int64_t batch) const {
+    const int64_t wb = p.kind == 1 ? p.rows * p.cols + 4 * p.rows : 4 * p.rows * p.cols;
+    return wb + 4 * batch * p.cols + 4 * batch * p.rows;
+  }
+
+  void gemv(const Proj& p, const float* x_in, int64_t ldx, float* out, int64_t ldo, int64_t batch, Epi epi) {
+    hipEvent_t b = nullptr;
+    begin(0, proj_bytes(p, batch), &b);
+    launch_gemv(p.kind, p.w.ptr, p.ld, p.kind == 1 ? p.s.as<float>() : nullptr, x_in, ldx, out, ldo, 1, p.rows, p.cols,
+                batch, epi, st());
+    end(b);
+  }
+
+  template <typename F>
+  void timed(int cls, int64_t bytes, F&& f) {
+    hipEvent_t b = nullptr;
+    begin(cls, bytes, &b);
+    f();
+    end(b);
+  }
+
+  void check_complete() const {
+    PIA_REQUIRE(embed_set && final_norm_set, "model: embedding and final norm must be set");
+    PIA_REQUIRE(lm_head.kind >= 0 && lm_head.filled == 1, "model: lm_head not set");
+    for (const auto& L : layers) {
+      PIA_REQUIRE(L.qkv.filled == 7 && L.o.filled == 1 && L.gu.filled == 3 && L.down.filled == 1,
+                  "model: every projection of every layer must be set");
+      PIA_REQUIRE(L.attn_norm.ptr && L.ffn_norm.ptr, "model: every layer norm must be set");
+    }
+    PIA_REQUIRE(kv.ptr != nullptr, "model: KV cache not allocated (pia_model_kv_alloc)");
+  }
+
+  // run_layers_batch (src/model.rs:968-1177) for `batch` rows whose step inputs are already on
+  // the device. Leaves the final normalized hidden state in xb.
+  void run_layers(int64_t batch, const int32_t* d_tokens, const pia_attn_entry* d_entries, const int32_t* d_tables,
+                  int64_t max_window, int64_t mapped_tokens) {
+    const auto& c = cfg;
+    const int64_t splits = attention_splits(std::max<int64_t>(1, max_window));
+    const int64_t wb = attention_work_bytes(batch, c.heads, hd, splits);
+    if (wb) attn_work.ensure(wb);
+    const int64_t attn_bytes = mapped_tokens * c.kv_heads * 2 * hd * 4 + 2 * batch * c.hidden * 4;
+    float* X = x.as<float>();
+    float* XB = xb.as<float>();
+    float* QKV = qkv.as<float>();
+    float* ATT = attn.as<float>();
+    float* GU = gu.as<float>();
+    float* H = h.as<float>();
+    timed(2, 0, [&] { launch_embed(d_tokens, embed.as<uint16_t>(), X, ld_h, batch, c.hidden, c.vocab, st()); });
+    for (int64_t l = 0; l < c.layers; ++l) {
+      Layer& L = layers[l];
+      timed(2, 0, [&] { launch_rmsnorm(X, ld_h, L.attn_norm.as<float>(), XB, ld_h, batch, c.hidden, c.rms_eps, st()); });
+      gemv(L.qkv, XB, ld_h, QKV, ld_qkv, batch, Epi::Store);
+      timed(2, 0, [&] {
+        launch_rope_kv_write(QKV, ld_qkv, d_entries, d_tables, rope_cos.as<float>(), rope_sin.as<float>(),
+                             kv.as<float>(), layout, c.heads, batch, l, st());
+      });
+      timed(1, attn_bytes, [&] {
+        launch_attention(QKV, ld_qkv, ATT, ld_h, kv.as<float>(), layout, c.heads, d_entries, d_tables, batch, l, splits,
+                         attn_work.ptr, st());
+      });
+      gemv(L.o, ATT, ld_h, X, ld_h, batch, Epi::Add);
+      timed(2, 0, [&] { launch_rmsnorm(X, ld_h, L.ffn_norm.as<float>(), XB, ld_h, batch, c.hidden, c.rms_eps, st()); });
+      gemv(L.gu, XB, ld_h, GU, ld_gu, batch, Epi::Store);
+      timed(2, 0, [&] { launch_swiglu(GU, ld_gu, H, ld_i, batch, c.inter, st()); });
+      gemv(L.down, H, ld_i, X, ld_h, batch, Epi::Add);
+    }
+    timed(2, 0, [&] { launch_rmsnorm(X, ld_h, final_norm.as<float>(), XB, ld_h, batch, c.hidden, c.rms_eps, st()); });
+  }
+
+  void finish_prof() {
+    for (int i = 0; i < 3; ++i) prof.ms[i] = 0, prof.bytes[i] = 0;
+    if (!prof.on) return;
+    PIA_HIP(hipStreamSynchronize(st()));
+    for (auto& r : prof.recs) {
+      float t = 0;
+      PIA_HIP(hipEventElapsedTime(&t, r.a, r.b));
+      prof.ms[r.cls] += t;
+      prof.bytes[r.cls] += r.bytes;
+    }
+    prof.reset();
+  }
+};
+
+namespace {
+
+void alloc_proj(Proj& p, int kind, int64_t rows, int64_t cols) {
+  p.kind = kind;
+  p.rows = rows;
+  p.cols = cols;
+  p.ld = round_up(cols, kind == 1 ? 16 : 4);
+  const int64_t esz = kind == 1 ? 1 : 4;
+  p.w.ensure(rows * p.ld * esz);
+  PIA_HIP(hipMemset(p.w.ptr, 0, rows * p.ld * esz));
+  if (kind == 1) p.s.ensure(rows * 4);
+  p.filled = 0;
+}
+
+// Copy `rows` host rows of `cols` into p at row offset r0, with row padding.
+void upload_rows(Proj& p, int64_t r0, int64_t rows, const void* src, const float* scales) {
+  const int64_t esz = p.kind == 1 ? 1 : 4;
+  PIA_HIP(hipMemcpy2D(static_cast<char*>(p.w.ptr) + r0 * p.ld * esz, p.ld * esz, src, p.cols * esz, p.cols * esz, rows,
+                      hipMemcpyHostToDevice));
+  if (p.kind == 1) PIA_HIP(hipMemcpy(p.s.as<float>() + r0, scales, rows * 4, hipMemcpyHostToDevice));
+}
+
+struct Target {
+  Proj* p;
+  int64_t r0, rows, cols;
+  uint32_t bit;
+};
+
+Target target_of(pia_model* m, int64_t layer, int32_t which) {
+  const auto& c = m->cfg;
+  if (which == PIA_LM_HEAD) return {&m->lm_head, 0, c.vocab, c.hidden, 1};
+  PIA_REQUIRE(layer >= 0 && layer < c.layers, "layer index out of range");
+  Layer& L = m->layers[layer];
+  switch (which) {
+    case PIA_WQ: return {&L.qkv, 0, c.hidden, c.hidden, 1};
+    case PIA_WK: return {&L.qkv, c.hidden, m->kvd, c.hidden, 2};
+    case PIA_WV: return {&L.qkv, c.hidden + m->kvd, m->kvd, c.hidden, 4};
+    case PIA_WO: return {&L.o, 0, c.hidden, c.hidden, 1};
+    case PIA_W1: return {&L.gu, 0, c.inter, c.hidden, 1};
+    case PIA_W3: return {&L.gu, c.inter, c.inter, c.hidden, 2};
+    case PIA_W2: return {&L.down, 0, c.hidden, c.inter, 1};
+    default: fail(PIA_ERR_INVALID, "unknown projection slot");
+  }
+}
+
+int64_t total_rows(pia_model* m, const Proj* p) {
+  const auto& c = m->cfg;
+  if (p == &m->lm_head) return c.vocab;
+  for (auto& L : m->layers) {
+    if (p == &L.qkv) return m->qkv_rows;
+    if (p == &L.o) return c.hidden;
+    if (p == &L.gu) return 2 * c.inter;
+    if (p == &L.down) return c.hidden;
+  }
+  return 0;
+}
+
+void set_proj(pia_model* m, int64_t layer, int32_t which, int kind, const void* data, const float* scales) {
+  PIA_REQUIRE(m && data, "null argument");
+  PIA_REQUIRE(kind == 0 || scales, "int8 projection needs scales");
+  Target t = target_of(m, layer, which);
+  PIA_HIP(hipSetDevice(m->ctx->device));
+  if (t.p->kind != kind) {
+    PIA_REQUIRE(t.p->filled == 0 || t.p->kind < 0,
+                "fused projection group mixes int8 and f32 slots; set every slot of the group with one kind");
+    alloc_proj(*t.p, kind, total_rows(m, t.p), t.cols);
+  }
+  upload_rows(*t.p, t.r0, t.rows, data, scales);
+  t.p->filled |= t.bit;
+}
+
+}  // namespace
+
+extern "C" {
+
+pia_status pia_model_create(pia_context* ctx, const pia_model_config* cfg, pia_model** out) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx && cfg && out, "null argument");
+  const auto& c = *cfg;
+  PIA_REQUIRE(c.hidden > 0 && c.layers > 0 && c.heads > 0 && c.kv_heads > 0 && c.inter > 0 && c.vocab > 0,
+              "model dimensions must be positive");
+  PIA_REQUIRE(c.hidden % c.heads == 0, "hidden_size must be a multiple of num_attention_heads");
+  PIA_REQUIRE(c.heads % c.kv_heads == 0, "num_attention_heads must be a multiple of num_key_value_heads");
+  auto* m = new pia_model;
+  m->ctx = ctx;
+  m->cfg = c;
+  m->hd = c.hidden / c.heads;
+  m->kvd = c.kv_heads * m->hd;
+  m->qkv_rows = c.hidden + 2 * m->kvd;
+  m->ld_h = round_up(c.hidden, 16);
+  m->ld_qkv = round_up(m->qkv_rows, 16);
+  m->ld_gu = round_up(2 * c.inter, 16);
+  m->ld_i = round_up(c.inter, 16);
+  m->ld_v = round_up(c.vocab, 16);
+  m->layers.resize(c.layers);
+  *out = m;
+  PIA_API_END
+}
+
+// Must run before the context's destruction (the model enqueues work on the context stream).
+pia_status pia_model_destroy(pia_model* m) {
+  if (m) {
+    (void)hipSetDevice(m->ctx->device);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    delete m;
+  }
+  return PIA_OK;
+}
+
+pia_status pia_model_set_embedding(pia_model* m, const uint16_t* bf16) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(m && bf16, "null argument");
+  const size_t bytes = static_cast<size_t>(m->cfg.vocab) * m->cfg.hidden * 2;
+  m->embed.ensure(bytes);
+  PIA_HIP(hipMemcpy(m->embed.ptr, bf16, bytes, hipMemcpyHostToDevice));
+  m->embed_set = true;
+  PIA_API_END
+}
+
+pia_status pia_model_set_norm(pia_model* m, int64_t layer, int32_t which, const float* w) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(m && w, "null argument");
+  DeviceBuffer* dst = nullptr;
+  if (which == PIA_NORM_FINAL) {
+    dst = &m->final_norm;
+    m->final_norm_set = true;
+  } else {
+    PIA_REQUIRE(layer >= 0 && layer < m->cfg.layers, "layer index out of range");
+    PIA_REQUIRE(which == PIA_NORM_ATTN || which == PIA_NORM_FFN, "unknown norm slot");
+    dst = which == PIA_NORM_ATTN ? &m->layers[layer].attn_norm : &m->layers[layer].ffn_norm;
+  }
+  dst->ensure(m->cfg.hidden * 4);
+  PIA_HIP(hipMemcpy(dst->ptr, w, m->cfg.hidden * 4, hipMemcpyHostToDevice));
+  PIA_API_END
+}
+
+pia_status pia_model_set_proj_i8(pia_model* m, int64_t layer, int32_t which, const int8_t* q, const float* scales) {
+  PIA_API_BEGIN
+  set_proj(m, layer, which, 1, q, scales);
+  PIA_API_END
+}
+
+pia_status pia_model_set_proj_f32(pia_model* m, int64_t layer, int32_t which, const float* w) {
+  PIA_API_BEGIN
+  set_proj(m, layer, which, 0, w, nullptr);
+  PIA_API_END
+}
+
+int64_t pia_model_weight_bytes(const pia_model* m) {
+  if (!m) return 0;
+  auto pb = [](const Proj& p) -> int64_t {
+    if (p.kind == 1) return p.rows * p.cols + 4 * p.rows;
+    if (p.kind == 0) return 4 * p.rows * p.cols;
+    return 0;
+  };
+  int64_t t = pb(m->lm_head);
+  for (const auto& L : m->layers) t += pb(L.qkv) + pb(L.o) + pb(L.gu) + pb(L.down);
+  return t;
+}
+
+pia_status pia_model_kv_alloc(pia_model* m, int64_t num_blocks, int64_t block_size) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(m && num_blocks > 0 && block_size > 0, "bad KV shape");
+  PIA_HIP(hipSetDevice(m->ctx->device));
+  m->layout = pia_kv_layout{m->cfg.layers, num_blocks, block_size, m->cfg.kv_heads, m->hd};
+  const size_t bytes = static_cast<size_t>(m->cfg.layers) * num_blocks * block_size * m->cfg.kv_heads * 2 * m->hd * 4;
+  m->kv.release();
+  m->kv.ensure(bytes);
+  PIA_HIP(hipMemset(m->kv.ptr, 0, bytes));
+  PIA_API_END
+}
+
+pia_status pia_model_kv(pia_model* m, float** kv, pia_kv_layout* layout) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(m, "null model");
+  if (kv) *kv = m->kv.as<float>();
+  if (layout) *layout = m->layout;
+  PIA_API_END
+}
+
+pia_status pia_model_profile(pia_model* m, int32_t enable) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(m, "null model");
+  m->prof.on = enable != 0;
+  PIA_API_END
+}
+
+pia_status pia_model_profile_get(pia_model* m, double* ms, int64_t* bytes, int32_t n) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(m, "null model");
+  for (int i = 0; i < n && i < 3; ++i) {
+    if (ms) ms[i] = m->prof.ms[i];
+    if (bytes) bytes[i] = m->prof.bytes[i];
+  }
+  PIA_API_END
+}
+
+}  // extern "C"
+
+namespace {
+
+int64_t window_start(int64_t pos, int64_t window) {
+  if (window < 0) return 0;
+  return pos + 1 > window ? pos + 1 - window : 0;
+}
+
+// Stage tokens, entries and tables in one pinned buffer and one host->device copy.
+struct StepInputs {
+  const int32_t* tokens;
+  const pia_attn_entry* entries;
+  const int32_t* tables;
+};
+
+StepInputs upload_step(pia_model* m, const std::vector<int32_t>& tok, const std::vector<pia_attn_entry>& ent,
+                       const int32_t* tables, int64_t ntab) {
+  const size_t n = tok.size();
+  const size_t off_e = round_up(n * 4, 64), off_t = off_e + round_up(n * sizeof(pia_attn_entry), 64);
+  const size_t total = off_t + round_up(std::max<int64_t>(ntab, 1) * 4, 64);
+  PIA_HIP(hipStreamSynchronize(m->st()));  // the pinned staging buffer may still be in flight
+  m->pin.ensure(total);
+  m->step.ensure(total);
+  char* p = static_cast<char*>(m->pin.ptr);
+  std::memcpy(p, tok.data(), n * 4);
+  std::memcpy(p + off_e, ent.data(), n * sizeof(pia_attn_entry));
+  if (ntab) std::memcpy(p + off_t, tables, ntab * 4);
+  PIA_HIP(hipMemcpyAsync(m->step.ptr, p, total, hipMemcpyHostToDevice, m->st()));
+  char* d = static_cast<char*>(m->step.ptr);
+  return {reinterpret_cast<const int32_t*>(d), reinterpret_cast<const pia_attn_entry*>(d + off_e),
+          reinterpret_cast<const int32_t*>(d + off_t)};
+}
+
+int64_t mapped_in_window(const pia_attn_entry& e, int64_t bs) {
+  // Tokens of start..=pos that fall inside mapped logical blocks (the K/V actually read).
+  const int64_t end = std::min<int64_t>(e.pos + 1, static_cast<int64_t>(e.table_len) * bs);
+  return std::max<int64_t>(0, end - e.start);
+}
+
+}  // namespace
+
+extern "C" {
+
+pia_status pia_model_decode(pia_model* m, const uint32_t* tokens, const int64_t* positions, const int64_t* table_off,
+                            const int64_t* table_len, const int32_t* tables, int64_t batch, float* logits,
+                            int32_t* argmax) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(m && tokens && positions && table_off && table_len, "null argument");
+  PIA_REQUIRE(batch > 0, "decode needs at least one sequence");
+  m->check_complete();
+  PIA_HIP(hipSetDevice(m->ctx->device));
+  const auto& c = m->cfg;
+  int64_t ntab = 0, max_pos = 0, max_window = 1, mapped = 0;
+  std::vector<int32_t> tok(batch);
+  std::vector<pia_attn_entry> ent(batch);
+  for (int64_t b = 0; b < batch; ++b) {
+    PIA_REQUIRE(positions[b] >= 0 && positions[b] < (int64_t(1) << 30), "position out of range");
+    PIA_REQUIRE(table_off[b] >= 0 && table_len[b] >= 0, "negative table offset/length");
+    ntab = std::max(ntab, table_off[b] + table_len[b]);
+    max_pos = std::max(max_pos, positions[b]);
+    tok[b] = static_cast<int32_t>(tokens[b]);
+    const int64_t st = window_start(positions[b], c.attention_window);
+    ent[b] = pia_attn_entry{static_cast<int32_t>(positions[b]), static_cast<int32_t>(st),
+                            static_cast<int32_t>(table_off[b]), static_cast<int32_t>(table_len[b])};
+    max_window = std::max(max_window, positions[b] + 1 - st);
+    mapped += mapped_in_window(ent[b], m->layout.block_size);
+  }
+  PIA_REQUIRE(ntab == 0 || tables, "null block tables");
+  for (int64_t i = 0; i < ntab; ++i)
+    PIA_REQUIRE(tables[i] >= 0 && tables[i] < m->layout.num_blocks, "block table entry out of range");
+  m->ensure_cap(batch);
+  m->ensure_rope(max_pos);
+  m->logits.ensure(batch * m->ld_v * 4);
+  StepInputs in = upload_step(m, tok, ent, tables, ntab);
+  m->prof.reset();
+  m->run_layers(batch, in.tokens, in.entries, in.tables, max_window, mapped);
+  m->gemv(m->lm_head, m->xb.as<float>(), m->ld_h, m->logits.as<float>(), m->ld_v, batch, Epi::Store);
+  m->timed(2, 0, [&] { launch_argmax(m->logits.as<float>(), m->ld_v, m->amax.as<int32_t>(), batch, c.vocab, m->st()); });
+  if (logits)
+    PIA_HIP(hipMemcpy2DAsync(logits, c.vocab * 4, m->logits.ptr, m->ld_v * 4, c.vocab * 4, batch,
+                             hipMemcpyDeviceToHost, m->st()));
+  if (argmax) PIA_HIP(hipMemcpyAsync(argmax, m->amax.ptr, batch * 4, hipMemcpyDeviceToHost, m->st()));
+  PIA_HIP(hipStreamSynchronize(m->st()));
+  m->finish_prof();
+  PIA_API_END
+}
+
+pia_status pia_model_prefill(pia_model* m, const uint32_t* tokens, int64_t n, int64_t start_pos, const int32_t* table,
+                             int64_t table_len, float* logits, int32_t* argmax) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(m && tokens, "null argument");
+  PIA_REQUIRE(n > 0, "prefill needs at least one token");
+  PIA_REQUIRE(start_pos >= 0 && start_pos + n < (int64_t(1) << 30), "position out of range");
+  PIA_REQUIRE(table_len >= 0 && (table_len == 0 || table), "bad block table");
+  m->check_complete();
+  PIA_HIP(hipSetDevice(m->ctx->device));
+  const auto& c = m->cfg;
+  for (int64_t i = 0; i < table_len; ++i)
+    PIA_REQUIRE(table[i] >= 0 && table[i] < m->layout.num_blocks, "block table entry out of range");
+  std::vector<int32_t> tok(n);
+  std::vector<pia_attn_entry> ent(n);
+  int64_t max_window = 1, mapped = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t pos = start_pos + i;
+    const int64_t st = window_start(pos, c.attention_window);
+    tok[i] = static_cast<int32_t>(tokens[i]);
+    ent[i] = pia_attn_entry{static_cast<int32_t>(pos), static_cast<int32_t>(st), 0, static_cast<int32_t>(table_len)};
+    max_window = std::max(max_window, pos + 1 - st);
+    mapped += mapped_in_window(ent[i], m->layout.block_size);
+  }
+  m->ensure_cap(n);
+  m->ensure_rope(start_pos + n);
+  m->logits.ensure(m->ld_v * 4);
+  StepInputs in = upload_step(m, tok, ent, table, table_len);
+  m->prof.reset();
+  m->run_layers(n, in.tokens, in.entries, in.tables, max_window, mapped);
+  // Only the last position pays for the LM head (src/model.rs:1249-1254).
+  m->gemv(m->lm_head, m->xb.as<float>() + (n - 1) * m->ld_h, m->ld_h, m->logits.as<float>(), m->ld_v, 1, Epi::Store);
+  m->timed(2, 0, [&] { launch_argmax(m->logits.as<float>(), m->ld_v, m->amax.as<int32_t>(), 1, c.vocab, m->st()); });
+  if (logits) PIA_HIP(hipMemcpyAsync(logits, m->logits.ptr, c.vocab * 4, hipMemcpyDeviceToHost, m->st()));
+  if (argmax) PIA_HIP(hipMemcpyAsync(argmax, m->amax.ptr, 4, hipMemcpyDeviceToHost, m->st()));
+  PIA_HIP(hipStreamSynchronize(m->st()));
+  m->finish_prof();
+  PIA_API_END
+}
+
+}  // extern "C"

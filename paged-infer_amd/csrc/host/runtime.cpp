@@ -1,0 +1,342 @@
+// Context, device-memory helpers and the kernel-tier C ABI (src/math.rs, src/attention.rs,
+// src/memory/layout.rs seams), plus the synthetic-input helpers.
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../common.h"
+#include "../kernels.h"
+#include "context.h"
+
+namespace pia {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void set_last_error(const std::string& msg) { g_last_error = msg; }
+
+hipStream_t stream_of(pia_context* ctx, void* stream) {
+  return stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+}
+
+DeviceBuffer::~DeviceBuffer() { release(); }
+
+void DeviceBuffer::release() {
+  if (ptr) (void)hipFree(ptr);
+  ptr = nullptr;
+  bytes = 0;
+}
+
+void DeviceBuffer::ensure(size_t need) {
+  if (need <= bytes) return;
+  release();
+  PIA_HIP(hipMalloc(&ptr, need));
+  bytes = need;
+}
+
+PinnedBuffer::~PinnedBuffer() {
+  if (ptr) (void)hipHostFree(ptr);
+}
+
+void PinnedBuffer::ensure(size_t need) {
+  if (need <= bytes) return;
+  if (ptr) (void)hipHostFree(ptr);
+  ptr = nullptr;
+  bytes = 0;
+  PIA_HIP(hipHostMalloc(&ptr, need, hipHostMallocDefault));
+  bytes = need;
+}
+
+void check_layout(const pia_kv_layout* L) {
+  PIA_REQUIRE(L != nullptr, "null kv layout");
+  PIA_REQUIRE(L->num_layers > 0 && L->num_blocks > 0 && L->block_size > 0 && L->num_kv_heads > 0 && L->head_dim > 0,
+              "kv layout dimensions must be positive");
+}
+
+// quantize_rows_i8 (src/math.rs:456-469) on the host, rows split over threads (each row is
+// independent, so the split changes no result).
+void quantize_rows_host(const float* w, int64_t rows, int64_t cols, int8_t* q, float* scales) {
+  auto body = [&](int64_t r0, int64_t r1) {
+    for (int64_t r = r0; r < r1; ++r) {
+      const float* row = w + r * cols;
+      float max_abs = 0.0f;
+      for (int64_t c = 0; c < cols; ++c) max_abs = std::fmax(max_abs, std::fabs(row[c]));
+      const float scale = max_abs > 0.0f ? max_abs / 127.0f : 1.0f;
+      scales[r] = scale;
+      int8_t* qr = q + r * cols;
+      for (int64_t c = 0; c < cols; ++c) {
+        float v = std::roundf(row[c] / scale);
+        v = std::fmin(std::fmax(v, -127.0f), 127.0f);
+        qr[c] = static_cast<int8_t>(v);
+      }
+    }
+  };
+  const int64_t work = rows * cols;
+  const unsigned nt = work < (int64_t(1) << 20) ? 1u : std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  if (nt == 1) {
+    body(0, rows);
+    return;
+  }
+  std::vector<std::thread> ts;
+  const int64_t per = (rows + nt - 1) / nt;
+  for (unsigned t = 0; t < nt; ++t) {
+    const int64_t r0 = t * per, r1 = std::min(rows, r0 + per);
+    if (r0 < r1) ts.emplace_back(body, r0, r1);
+  }
+  for (auto& t : ts) t.join();
+}
+
+}  // namespace pia
+
+using namespace pia;
+
+extern "C" {
+
+const char* pia_last_error(void) { return g_last_error.c_str(); }
+const char* pia_version(void) { return "paged-infer-amd 0.1 (gfx950)"; }
+
+pia_status pia_context_create(int device, pia_context** out) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(out != nullptr, "null output pointer");
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) fail(PIA_ERR_NO_DEVICE, "no HIP device available");
+  PIA_REQUIRE(device >= 0 && device < n, "device index out of range");
+  PIA_HIP(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  PIA_HIP(hipGetDeviceProperties(&prop, device));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    fail(PIA_ERR_NO_DEVICE, std::string("this library is built for gfx950; device is ") + prop.gcnArchName);
+  auto* ctx = new pia_context;
+  ctx->device = device;
+  ctx->num_cus = prop.multiProcessorCount;
+  PIA_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+  *out = ctx;
+  PIA_API_END
+}
+
+pia_status pia_context_destroy(pia_context* ctx) {
+  PIA_API_BEGIN
+  if (!ctx) return PIA_OK;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+  PIA_API_END
+}
+
+pia_status pia_context_synchronize(pia_context* ctx) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx, "null context");
+  PIA_HIP(hipStreamSynchronize(ctx->stream));
+  PIA_API_END
+}
+
+void* pia_context_stream(pia_context* ctx) { return ctx ? static_cast<void*>(ctx->stream) : nullptr; }
+
+pia_status pia_malloc(pia_context* ctx, size_t bytes, void** dptr) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx && dptr, "null argument");
+  PIA_HIP(hipSetDevice(ctx->device));
+  PIA_HIP(hipMalloc(dptr, bytes ? bytes : 1));
+  PIA_API_END
+}
+
+pia_status pia_free(pia_context* ctx, void* dptr) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx, "null context");
+  if (dptr) PIA_HIP(hipFree(dptr));
+  PIA_API_END
+}
+
+pia_status pia_memcpy_h2d(pia_context* ctx, void* dst, const void* src, size_t bytes) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx, "null context");
+  PIA_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  PIA_HIP(hipStreamSynchronize(ctx->stream));
+  PIA_API_END
+}
+
+pia_status pia_memcpy_d2h(pia_context* ctx, void* dst, const void* src, size_t bytes) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx, "null context");
+  PIA_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  PIA_HIP(hipStreamSynchronize(ctx->stream));
+  PIA_API_END
+}
+
+pia_status pia_quantize_rows_i8(const float* w, int64_t rows, int64_t cols, int8_t* q, float* scales) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(rows >= 0 && cols >= 0, "negative shape");
+  PIA_REQUIRE(rows == 0 || cols == 0 || (w && q && scales), "null argument");
+  quantize_rows_host(w, rows, cols, q, scales);
+  PIA_API_END
+}
+
+pia_status pia_quantize_rows_i8_dev(pia_context* ctx, const float* w, int64_t rows, int64_t cols, int8_t* q,
+                                    float* scales, void* stream) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx, "null context");
+  PIA_REQUIRE(rows >= 0 && cols >= 0, "negative shape");
+  launch_quantize_rows(w, rows, cols, q, scales, stream_of(ctx, stream));
+  PIA_API_END
+}
+
+pia_status pia_matvec_i8_dev(pia_context* ctx, float* out, const float* x, const int8_t* w, const float* scales,
+                             int64_t rows, int64_t cols, void* stream) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx && out && x && w && scales, "null argument");
+  launch_gemv(1, w, cols, scales, x, cols, out, 0, 1, rows, cols, 1, Epi::Store, stream_of(ctx, stream));
+  PIA_API_END
+}
+
+pia_status pia_matmat_i8_dev(pia_context* ctx, float* out_rb, const float* x_br, const int8_t* w,
+                             const float* scales, int64_t batch, int64_t rows, int64_t cols, void* stream) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx && out_rb && x_br && w && scales, "null argument");
+  launch_gemv(1, w, cols, scales, x_br, cols, out_rb, 1, batch, rows, cols, batch, Epi::Store, stream_of(ctx, stream));
+  PIA_API_END
+}
+
+pia_status pia_qlinear_apply_dev(pia_context* ctx, float* out_br, const float* x_br, const int8_t* w,
+                                 const float* scales, int64_t batch, int64_t rows, int64_t cols, void* stream) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx && out_br && x_br && w && scales, "null argument");
+  launch_gemv(1, w, cols, scales, x_br, cols, out_br, rows, 1, rows, cols, batch, Epi::Store, stream_of(ctx, stream));
+  PIA_API_END
+}
+
+pia_status pia_matvec_i8(pia_context* ctx, float* out, const float* x, const int8_t* w, const float* scales,
+                         int64_t rows, int64_t cols) {
+  return pia_matmat_i8(ctx, out, x, w, scales, 1, rows, cols);
+}
+
+pia_status pia_matmat_i8(pia_context* ctx, float* out_rb, const float* x_br, const int8_t* w, const float* scales,
+                         int64_t batch, int64_t rows, int64_t cols) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx && out_rb && x_br && w && scales, "null argument");
+  PIA_REQUIRE(rows > 0 && cols > 0 && batch > 0, "empty shape");
+  PIA_HIP(hipSetDevice(ctx->device));
+  DeviceBuffer dw, ds, dx, dout;
+  dw.ensure(rows * cols);
+  ds.ensure(rows * sizeof(float));
+  dx.ensure(batch * cols * sizeof(float));
+  dout.ensure(batch * rows * sizeof(float));
+  hipStream_t st = ctx->stream;
+  PIA_HIP(hipMemcpyAsync(dw.ptr, w, rows * cols, hipMemcpyHostToDevice, st));
+  PIA_HIP(hipMemcpyAsync(ds.ptr, scales, rows * sizeof(float), hipMemcpyHostToDevice, st));
+  PIA_HIP(hipMemcpyAsync(dx.ptr, x_br, batch * cols * sizeof(float), hipMemcpyHostToDevice, st));
+  launch_gemv(1, dw.ptr, cols, static_cast<const float*>(ds.ptr), static_cast<const float*>(dx.ptr), cols,
+              static_cast<float*>(dout.ptr), 1, batch, rows, cols, batch, Epi::Store, st);
+  PIA_HIP(hipMemcpyAsync(out_rb, dout.ptr, batch * rows * sizeof(float), hipMemcpyDeviceToHost, st));
+  PIA_HIP(hipStreamSynchronize(st));
+  PIA_API_END
+}
+
+pia_status pia_paged_attention_dev(pia_context* ctx, float* out, const float* q, const float* kv,
+                                   const pia_kv_layout* layout, int64_t num_heads, const pia_attn_entry* entries,
+                                   const int32_t* tables, int64_t n, int64_t layer, void* stream) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx, "null context");
+  check_layout(layout);
+  PIA_REQUIRE(n >= 0, "negative entry count");
+  if (n == 0) return PIA_OK;
+  PIA_REQUIRE(out && q && kv && entries, "null argument");
+  // Entries live on the device; the split count must cover the widest window, which the host
+  // bounds by the cache capacity (every window is at most num_blocks * block_size ... plus
+  // unmapped tail positions up to the entry's pos). Read the entries back once to size it.
+  std::vector<pia_attn_entry> host(n);
+  hipStream_t st = stream_of(ctx, stream);
+  PIA_HIP(hipMemcpyAsync(host.data(), entries, n * sizeof(pia_attn_entry), hipMemcpyDeviceToHost, st));
+  PIA_HIP(hipStreamSynchronize(st));
+  int64_t widest = 1;
+  for (const auto& e : host) {
+    PIA_REQUIRE(e.pos >= 0 && e.start >= 0 && e.table_len >= 0 && e.table_off >= 0, "attention: negative entry field");
+    widest = std::max<int64_t>(widest, e.pos + 1 - e.start);
+  }
+  const int64_t hd = layout->head_dim;
+  const int64_t splits = attention_splits(widest);
+  DeviceBuffer work;
+  const int64_t wb = attention_work_bytes(n, num_heads, hd, splits);
+  if (wb) work.ensure(wb);
+  launch_attention(q, num_heads * hd, out, num_heads * hd, kv, *layout, num_heads, entries, tables, n, layer, splits,
+                   work.ptr, st);
+  PIA_HIP(hipStreamSynchronize(st));
+  PIA_API_END
+}
+
+pia_status pia_kv_copy_block_dev(pia_context* ctx, float* kv, const pia_kv_layout* layout, int64_t src, int64_t dst,
+                                 void* stream) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx && kv, "null argument");
+  check_layout(layout);
+  launch_copy_block(kv, *layout, src, dst, stream_of(ctx, stream));
+  PIA_API_END
+}
+
+pia_status pia_argmax_dev(pia_context* ctx, int32_t* out, const float* logits, int64_t n, int64_t vocab, void* stream) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx && out && logits, "null argument");
+  PIA_REQUIRE(vocab > 0, "empty vocabulary");
+  launch_argmax(logits, vocab, out, n, vocab, stream_of(ctx, stream));
+  PIA_API_END
+}
+
+// SplitMix64 stream -> Box-Muller in f64 -> f32. Deterministic for (seed, stream, index).
+pia_status pia_synth_normal(uint64_t seed, uint64_t stream, float std_dev, float* out, int64_t n) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(n >= 0 && (n == 0 || out), "bad output");
+  auto body = [=](int64_t i0, int64_t i1) {
+    auto mix = [](uint64_t z) {
+      z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+      z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+      return z ^ (z >> 31);
+    };
+    const uint64_t key = mix(seed ^ mix(stream + 0x9E3779B97F4A7C15ull));
+    for (int64_t i = i0 & ~int64_t(1); i < i1; i += 2) {
+      const uint64_t pair = static_cast<uint64_t>(i) >> 1;
+      const uint64_t a = mix(key + 2 * pair * 0x9E3779B97F4A7C15ull);
+      const uint64_t b = mix(key + (2 * pair + 1) * 0x9E3779B97F4A7C15ull);
+      const double u1 = (static_cast<double>(a >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+      const double u2 = static_cast<double>(b >> 11) * (1.0 / 9007199254740992.0);
+      const double r = std::sqrt(-2.0 * std::log(u1));
+      const double t = 6.283185307179586 * u2;
+      if (i >= i0 && i < i1) out[i] = static_cast<float>(r * std::cos(t) * std_dev);
+      if (i + 1 >= i0 && i + 1 < i1) out[i + 1] = static_cast<float>(r * std::sin(t) * std_dev);
+    }
+  };
+  const unsigned nt = n < (int64_t(1) << 20) ? 1u : std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  if (nt == 1) {
+    body(0, n);
+  } else {
+    std::vector<std::thread> ts;
+    const int64_t per = ((n + nt - 1) / nt + 1) & ~int64_t(1);
+    for (unsigned t = 0; t < nt; ++t) {
+      const int64_t i0 = t * per, i1 = std::min(n, i0 + per);
+      if (i0 < i1) ts.emplace_back(body, i0, i1);
+    }
+    for (auto& t : ts) t.join();
+  }
+  PIA_API_END
+}
+
+pia_status pia_f32_to_bf16(const float* in, uint16_t* out, int64_t n) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(n >= 0 && (n == 0 || (in && out)), "bad argument");
+  for (int64_t i = 0; i < n; ++i) {
+    uint32_t u;
+    std::memcpy(&u, &in[i], 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+      out[i] = static_cast<uint16_t>((u >> 16) | 0x40);  // quiet NaN
+    } else {
+      const uint32_t rounding = 0x7fffu + ((u >> 16) & 1u);
+      out[i] = static_cast<uint16_t>((u + rounding) >> 16);
+    }
+  }
+  PIA_API_END
+}
+
+}  // extern "C"

@@ -1,0 +1,143 @@
+"""GPU kernel parity through the C ABI against the CPU oracle on the same seeded inputs.
+Integer / index work (quantizer, block copy, argmax, block mapping) must be bit-exact; the
+f32 projections and attention may differ from the reference's summation order only by
+rounding, bounded here relative to sum(|w*x|) (projections) or 1e-5 (attention)."""
+import numpy as np
+import pytest
+
+import pia
+from oracle import memory as om
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _proj_case(rng, rows, cols, batch):
+    w = rng.normal(0, 0.02, (rows, cols)).astype(np.float32)
+    q, s = pia.quantize_rows_i8(w)
+    x = rng.normal(0, 1, (batch, cols)).astype(np.float32)
+    return q, s, x
+
+
+def _proj_bound(q, s, x):
+    # |f32 dot in any order - exact| <= cols * 2^-24 * sum|q x| (x2 for the scale rounding).
+    mag = np.abs(x.astype(np.float64)) @ np.abs(q.astype(np.float64)).T * s.astype(np.float64)[None, :]
+    return 2.0 * q.shape[1] * 2.0 ** -24 * mag + 1e-30
+
+
+SHAPES = [(1, 1, 1), (3, 7, 2), (17, 33, 3), (344, 128, 1), (128, 344, 5), (64, 129, 8), (2560, 2048, 1),
+          (2048, 5632, 1), (11264, 2048, 2), (1000, 2048, 13), (333, 4096, 32), (32000, 2048, 1)]
+
+
+@pytest.mark.parametrize("rows,cols,batch", SHAPES)
+def test_int8_projection_matches_oracle(ctx, rows, cols, batch):
+    print(f"[gemv] rows={rows} cols={cols} batch={batch}", flush=True)
+    rng = np.random.default_rng(rows * 7 + cols + batch)
+    q, s, x = _proj_case(rng, rows, cols, batch)
+    ref = orc.matmat_i8(q, s, x)  # [row][batch]
+    dq, ds, dx = ctx.to_device(q), ctx.to_device(s), ctx.to_device(x)
+    out_rb = ctx.empty((rows, batch), np.float32)
+    pia.check(pia.lib().pia_matmat_i8_dev(ctx.h, out_rb.ptr, dx.ptr, dq.ptr, ds.ptr, batch, rows, cols, None))
+    out_br = ctx.empty((batch, rows), np.float32)
+    pia.check(pia.lib().pia_qlinear_apply_dev(ctx.h, out_br.ptr, dx.ptr, dq.ptr, ds.ptr, batch, rows, cols, None))
+    ctx.sync()
+    bound = _proj_bound(q, s, x).T  # [row][batch]
+    got_rb = out_rb.numpy()
+    assert np.all(np.abs(got_rb - ref) <= bound)
+    assert np.array_equal(out_br.numpy(), got_rb.T)
+    if batch == 1:
+        out = np.empty(rows, np.float32)
+        pia.check(pia.lib().pia_matvec_i8(ctx.h, pia.ptr(out), pia.ptr(x[0]), pia.ptr(q), pia.ptr(s), rows, cols))
+        assert np.array_equal(out, got_rb[:, 0])
+
+
+def test_device_quantizer_bit_exact(ctx):
+    rng = np.random.default_rng(5)
+    for w in [rng.normal(0, 0.02, (300, 2048)), np.zeros((2, 33)), rng.integers(-500, 500, (7, 100)) / 8.0]:
+        w = w.astype(np.float32)
+        q_ref, s_ref = orc.quantize_rows_i8(w)
+        dw = ctx.to_device(w)
+        dq, ds = ctx.empty(w.shape, np.int8), ctx.empty((w.shape[0],), np.float32)
+        pia.check(pia.lib().pia_quantize_rows_i8_dev(ctx.h, dw.ptr, w.shape[0], w.shape[1], dq.ptr, ds.ptr, None))
+        ctx.sync()
+        assert np.array_equal(dq.numpy(), q_ref)
+        assert np.array_equal(ds.numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+def _attn_entries(entries, tables):
+    off, ln, flat = orc.flatten_tables(tables)
+    arr = np.zeros((len(entries), 4), np.int32)
+    for i, (pos, start) in enumerate(entries):
+        arr[i] = (pos, start, off[i], ln[i])
+    return arr, flat
+
+
+ATTN = [  # heads, kv_heads, head_dim, block_size, windows
+    (8, 2, 4, 8, [(33, 0), (40, 0), (20, 0)]),
+    (4, 2, 24, 16, [(39, 0), (5, 0)]),
+    (32, 4, 64, 16, [(700, 0), (129, 0), (255, 0), (256, 0), (1500, 0)]),
+    (32, 8, 128, 16, [(1300, 0), (17, 0)]),
+    (16, 16, 32, 4, [(63, 0), (10, 3), (5, 6)]),
+]
+
+
+@pytest.mark.parametrize("case", range(len(ATTN)))
+def test_paged_attention_matches_oracle(ctx, case):
+    heads, hkv, hd, bs, entries = ATTN[case]
+    print(f"[attention] heads={heads} kv={hkv} hd={hd} bs={bs} entries={entries}", flush=True)
+    rng = np.random.default_rng(case)
+    layers = 2
+    need = [(pos + bs) // bs for pos, _ in entries]
+    nblocks = sum(need) + 3
+    layout = (layers, nblocks, bs, hkv, hd)
+    kv = rng.uniform(-1.3, 1.6, layers * nblocks * bs * hkv * 2 * hd).astype(np.float32)
+    perm = rng.permutation(nblocks).tolist()
+    tables, k = [], 0
+    for i, n in enumerate(need):
+        mapped = n if i != 1 else max(1, n // 2)  # entry 1 leaves its tail unmapped
+        tables.append(perm[k:k + mapped])
+        k += n
+    q = rng.normal(0, 1, (len(entries), heads * hd)).astype(np.float32)
+    ref = orc.paged_attention(q, kv, layout, heads, entries, tables, 1)
+    ent, flat = _attn_entries(entries, tables)
+    dq, dkv, de, dt = ctx.to_device(q), ctx.to_device(kv), ctx.to_device(ent), ctx.to_device(flat)
+    out = ctx.empty(q.shape, np.float32)
+    L = pia.KvLayout(*layout)
+    pia.check(pia.lib().pia_paged_attention_dev(ctx.h, out.ptr, dq.ptr, dkv.ptr, L, heads, de.ptr, dt.ptr,
+                                                len(entries), 1, None))
+    got = out.numpy()
+    assert np.allclose(got, ref, atol=1e-5, rtol=1e-5), np.max(np.abs(got - ref))
+
+
+def test_copy_block_and_device_cow(ctx):
+    layout = (3, 4, 2, 2, 4)
+    L = pia.KvLayout(*layout)
+    kv = np.arange(np.prod(layout) * 2, dtype=np.float32)
+    for src, dst in [(1, 3), (3, 1)]:
+        dkv = ctx.to_device(kv)
+        pia.check(pia.lib().pia_kv_copy_block_dev(ctx.h, dkv.ptr, L, src, dst, None))
+        ref = kv.copy()
+        om.KvLayout(*layout).copy_block(ref, src, dst)
+        assert np.array_equal(dkv.numpy(), ref)
+    # ensure_writable moves block data on the device (kv_cache_manager.rs:289-327).
+    m = pia.KvCacheManager(4, 2)
+    t, _ = m.admit(1, [1, 2, 3], 1)
+    c = m.fork(t, 2, 2)
+    dkv = ctx.to_device(kv)
+    assert m.ensure_writable(2, c, 3, ctx, dkv.ptr, L)
+    ctx.sync()
+    ref = kv.copy()
+    om.KvLayout(*layout).copy_block(ref, t.blocks()[1], c.blocks()[1])
+    assert np.array_equal(dkv.numpy(), ref)
+
+
+def test_argmax_ties_total_order(ctx):
+    rows = np.array([[1, 3, 3, 2], [0.0, -0.0, -1, -2], [-0.0, 0.0, -1, -2], [-5, -4, -4, -7]], np.float32)
+    big = np.random.default_rng(0).normal(0, 1, (3, 32000)).astype(np.float32)
+    big[1, [5, 31999]] = 100.0
+    for logits in (rows, big):
+        d = ctx.to_device(logits)
+        out = ctx.empty((logits.shape[0],), np.int32)
+        pia.check(pia.lib().pia_argmax_dev(ctx.h, out.ptr, d.ptr, logits.shape[0], logits.shape[1], None))
+        ctx.sync()
+        assert out.numpy().tolist() == [orc.argmax(r) for r in logits]

@@ -1,0 +1,211 @@
+"""End-to-end parity of the GPU forward pass (C ABI model tier) with the CPU oracle and with
+the reference's golden fixture.
+
+Bar: greedy token sequences bit-exact vs the CPU reference path
+on the same seeded inputs; logits within max|delta| <= 2e-3 relative to the logit scale
+(max |logit| of the reference row); block tables and copy-on-write counts bit-exact. The
+golden fixture (f32 projections) uses the reference's own bar: max|delta| < 5e-4 and 0
+argmax mismatches over 40 positions (tests/golden_parity_tests.rs)."""
+import numpy as np
+import pytest
+
+import pia
+from golden import fixture
+from oracle import memory as om
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+LOGIT_TOL = 2e-3
+
+
+def _rel(a, b):
+    return float(np.max(np.abs(a - b)) / max(1e-30, np.max(np.abs(b))))
+
+
+def greedy_session(ctx, cfg, weights, prompt, steps, block_size=16):
+    """Prefill `prompt`, then `steps` greedy decode steps at batch 1, independently on the GPU
+    and on the oracle (each side feeds back its own argmax)."""
+    n_tok = len(prompt) + steps
+    nb = (n_tok + block_size - 1) // block_size
+    table = list(range(nb))  # a fresh FIFO pool hands out 0..nb-1
+    gm = pia.Model(ctx, cfg, weights)
+    gm.kv_alloc(nb + 1, block_size)
+    om_ = orc.OracleModel(cfg, weights)
+    kv = np.zeros(orc.kv_floats(cfg, nb + 1, block_size), np.float32)
+    lg, tg = gm.prefill(prompt, 0, table)
+    lc = om_.prefill(prompt, 0, table, kv, nb + 1, block_size)
+    tc = orc.argmax(lc)
+    rels = [_rel(lg, lc)]
+    gtoks, ctoks = [tg], [tc]
+    for i in range(steps - 1):
+        pos = len(prompt) + i
+        lg, am = gm.decode([gtoks[-1]], [pos], [table])
+        lc = om_.decode([ctoks[-1]], [pos], [table], kv, nb + 1, block_size)
+        if gtoks == ctoks:
+            rels.append(_rel(lg[0], lc[0]))
+        gtoks.append(int(am[0]))
+        ctoks.append(orc.argmax(lc[0]))
+    gm.close()
+    return gtoks, ctoks, max(rels)
+
+
+def test_golden_fixture_f32_on_gpu(ctx):
+    cfg, tokens, golden, weights = fixture.load()
+    cfg = pia.LlamaConfig(**cfg)
+    gm = pia.Model(ctx, cfg, weights)
+    gm.kv_alloc(8, fixture.BLOCK_SIZE)
+    table = [0, 1, 2]
+    rows = [gm.decode([t], [p], [table])[0][0] for p, t in enumerate(tokens)]
+    max_abs, mism = fixture.compare(np.stack(rows), golden)
+    print(f"golden incremental decode on GPU: max|delta|={max_abs:.3g} mismatches={mism}")
+    assert mism == 0 and max_abs < 5e-4
+    gm.kv_alloc(8, fixture.BLOCK_SIZE)
+    lg, _ = gm.prefill(tokens, 0, table)
+    max_abs, mism = fixture.compare(lg, golden[-1])
+    assert mism == 0 and max_abs < 5e-4
+    gm.kv_alloc(8, fixture.BLOCK_SIZE)
+    gm.prefill(tokens[:16], 0, table)
+    split, _ = gm.prefill(tokens[16:], 16, table)
+    assert np.max(np.abs(split - lg)) < 1e-5
+
+
+def test_config1_tiny_int8_greedy_parity(ctx):
+    """dim 128, 2 layers, 4/2 heads, FFN 344, vocab 512, block 16, 48-token
+    prompt, 40 greedy steps, int8 projections incl. lm_head."""
+    cfg = pia.TINY_C1
+    w = pia.synth_weights(cfg, seed=1)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab, 48).tolist()
+    g, c, rel = greedy_session(ctx, cfg, w, prompt, 40)
+    print(f"config1: rel max|dlogit|={rel:.3g} tokens={g[:10]}...")
+    assert g == c
+    assert rel <= LOGIT_TOL
+
+
+def test_config1_f32_lm_head_variant(ctx):
+    # The reference keeps lm_head f32 by default (src/model.rs:441-444).
+    cfg = pia.TINY_C1
+    w = pia.synth_weights(cfg, seed=2, lm_head_int8=False)
+    prompt = np.random.default_rng(2).integers(0, cfg.vocab, 48).tolist()
+    g, c, rel = greedy_session(ctx, cfg, w, prompt, 40)
+    assert g == c and rel <= LOGIT_TOL
+
+
+def test_sliding_window_model(ctx):
+    cfg = pia.LlamaConfig(hidden=128, layers=2, heads=4, kv_heads=2, inter=344, vocab=512, attention_window=20)
+    w = pia.synth_weights(cfg, seed=3)
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab, 37).tolist()
+    g, c, rel = greedy_session(ctx, cfg, w, prompt, 12)
+    assert g == c and rel <= LOGIT_TOL
+
+
+@pytest.mark.slow
+def test_config2_tinyllama_b1_greedy_parity(ctx):
+    """TinyLlama-1.1B shape, int8 (incl. lm_head), 512-token random prompt,
+    256 greedy decode steps at batch 1; greedy tokens bit-exact vs the CPU reference path."""
+    cfg = pia.TINYLLAMA
+    print("[config2] building weights", flush=True)
+    w = pia.synth_weights(cfg, seed=2024)
+    prompt = np.random.default_rng(2024).integers(0, cfg.vocab, 512).tolist()
+    print("[config2] running GPU + oracle sessions", flush=True)
+    g, c, rel = greedy_session(ctx, cfg, w, prompt, 256)
+    print(f"config2: rel max|dlogit|={rel:.3g} first tokens {g[:8]}")
+    assert g == c
+    assert rel <= LOGIT_TOL
+
+
+def test_config3_shape_batched_paged_decode(ctx):
+    """BASELINE config 3 shape: TinyLlama, batch 32, contexts U[128, 2048] from the seed, KV
+    blocks of 16 assigned by a random permutation of the pool; the KV history is synthetic
+    (seeded) and identical on both sides; 3 greedy steps."""
+    cfg = pia.TINYLLAMA
+    rng = np.random.default_rng(33)
+    B, steps, bs = 32, 3, 16
+    ctxs = rng.integers(128, 2049, B)
+    need = [(int(c) + steps + bs - 1) // bs for c in ctxs]
+    nb = sum(need)
+    perm = rng.permutation(nb).tolist()
+    tables, k = [], 0
+    for n in need:
+        tables.append(perm[k:k + n])
+        k += n
+    print(f"[config3] {nb} blocks, building weights", flush=True)
+    w = pia.synth_weights(cfg, seed=33)
+    kv = (rng.standard_normal(orc.kv_floats(cfg, nb, bs), dtype=np.float32) * 0.5)
+    gm = pia.Model(ctx, cfg, w)
+    gm.kv_alloc(nb, bs)
+    gm.kv_upload(kv)
+    om_ = orc.OracleModel(cfg, w)
+    toks_g = rng.integers(0, cfg.vocab, B).tolist()
+    toks_c = list(toks_g)
+    for s in range(steps):
+        pos = [int(c) + s for c in ctxs]
+        lg, am = gm.decode(toks_g, pos, tables)
+        lc = om_.decode(toks_c, pos, tables, kv, nb, bs)
+        rel = max(_rel(lg[b], lc[b]) for b in range(B))
+        toks_g = am.tolist()
+        toks_c = [orc.argmax(r) for r in lc]
+        print(f"[config3] step {s} rel={rel:.3g}", flush=True)
+        assert toks_g == toks_c
+        assert rel <= LOGIT_TOL
+    # The decode writes landed in the same slots (values differ only by projection rounding).
+    assert np.allclose(gm.kv_download(), kv, rtol=1e-4, atol=1e-5)
+    gm.close()
+
+
+def test_prefix_sharing_and_cow_workload(ctx):
+    """Config-5 workload in miniature (config-1 shapes): shared prefixes mapped through the
+    prefix cache, forks whose first write copies the shared tail block, batched greedy decode.
+    Block tables, COW counts and tokens bit-exact between (product manager + GPU model) and
+    (oracle manager + oracle model)."""
+    cfg = pia.TINY_C1
+    w = pia.synth_weights(cfg, seed=5)
+    bs, total = 16, 64
+    rng = np.random.default_rng(5)
+    prefixes = [rng.integers(0, cfg.vocab, 40).tolist() for _ in range(2)]
+    gm = pia.Model(ctx, cfg, w)
+    gm.kv_alloc(total, bs)
+    kvp, lay = gm.kv_ptr, gm.layout
+    om_ = orc.OracleModel(cfg, w)
+    kv = np.zeros(orc.kv_floats(cfg, total, bs), np.float32)
+    olay = om.KvLayout(cfg.layers, total, bs, cfg.kv_heads, cfg.head_dim)
+    mg, mo = pia.KvCacheManager(total, bs), om.KvCacheManager(total, bs)
+    seqs = []  # (seq_id, gpu_table, oracle_table, next_pos, gpu_tok, cpu_tok)
+    sid, tick = 0, 0
+    for pfx in prefixes:
+        for rep in range(2):  # second admission of the same prompt hits the prefix cache
+            tick += 1
+            tg, info = mg.admit(sid, pfx, tick)
+            ao = mo.admit(sid, pfx, tick)
+            assert tg.blocks() == ao.table.blocks() and info[0] == ao.cached_tokens
+            resume = min(info[0], len(pfx) - 1)
+            lg, _ = gm.prefill(pfx[resume:], resume, tg.blocks())
+            lc = om_.prefill(pfx[resume:], resume, ao.table.blocks(), kv, total, bs)
+            assert _rel(lg, lc) <= LOGIT_TOL
+            assert mg.publish(tg) == mo.publish_prompt_blocks(ao.table)
+            seqs.append([sid, tg, ao.table, len(pfx), orc.argmax(lg), orc.argmax(lc)])
+            sid += 1
+            # Fork one child off each admitted sequence: it shares the partial tail block.
+            tick += 1
+            cg = mg.fork(tg, sid, tick)
+            co = mo.fork(ao.table, sid, tick)
+            seqs.append([sid, cg, co, len(pfx), seqs[-1][4], seqs[-1][5]])
+            sid += 1
+    for step in range(6):
+        tick += 1
+        for s in seqs:
+            seq_id, tg, to, pos = s[0], s[1], s[2], s[3]
+            while len(tg) * bs <= pos:
+                assert mg.append_block(seq_id, tg, tick) == mo.append_block(seq_id, to, tick)
+            cg = mg.ensure_writable(seq_id, tg, pos, ctx, kvp, lay)
+            co = mo.ensure_writable(seq_id, to, pos, lambda a, b: olay.copy_block(kv, a, b))
+            assert cg == co and tg.blocks() == to.blocks()
+        lg, am = gm.decode([s[4] for s in seqs], [s[3] for s in seqs], [s[1].blocks() for s in seqs])
+        lc = om_.decode([s[5] for s in seqs], [s[3] for s in seqs], [s[2].blocks() for s in seqs], kv, total, bs)
+        for b, s in enumerate(seqs):
+            assert int(am[b]) == orc.argmax(lc[b])
+            assert _rel(lg[b], lc[b]) <= LOGIT_TOL
+            s[4], s[5], s[3] = int(am[b]), orc.argmax(lc[b]), s[3] + 1
+    assert mg.stats()["cow_copies"] == mo.cow_copies > 0
+    assert mg.stats()["hits"] == mo.cache.hits
+    assert np.allclose(gm.kv_download(), kv, rtol=1e-4, atol=1e-5)
+    gm.close()
