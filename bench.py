@@ -55,6 +55,25 @@ def decode_loop(model, toks, positions, tables, steps, bs, mgr=None):
     return toks, positions
 
 
+def profile_pass(model, toks, pos, tables, steps):
+    """Per-kernel-class device time of `steps` decode steps (HIP events around every launch on
+    the library's stream, eager launches behind a short device spin so the events bracket only
+    their kernel). Same inputs and kernels as the timed graph replays."""
+    model.profile(True)
+    acc = np.zeros(3)
+    by = np.zeros(3)
+    for _ in range(steps):
+        _, am = model.decode(toks, pos, tables, want_logits=False)
+        ms, b = model.profile_get()
+        acc += ms
+        by += b
+        toks = am.tolist()
+        pos = [p + 1 for p in pos]
+    model.profile(False)
+    return dict(gemv_ms=acc[0] / steps, attn_ms=acc[1] / steps, other_ms=acc[2] / steps, gemv_bytes=by[0] / steps,
+                attn_bytes=by[1] / steps)
+
+
 def run_b1(ctx, cfg, weights, steps, warmup, prompt_len=512):
     bs = 16
     total_tokens = prompt_len + warmup + 2 * steps + 8
@@ -68,30 +87,16 @@ def run_b1(ctx, cfg, weights, steps, warmup, prompt_len=512):
     ctx.sync()
     prefill_s = time.perf_counter() - t0
     toks, pos = decode_loop(model, [tok], [prompt_len], [table], warmup, bs)
-    # Timed region: K decode steps, per-kernel HIP events recorded on the library stream.
-    model.profile(True)
-    gemv_ms = attn_ms = other_ms = 0.0
-    gemv_bytes = attn_bytes = 0
+    # Timed region: K greedy decode steps, each a replay of the captured decode graph.
     ctx.sync()
     t0 = time.perf_counter()
-    for _ in range(steps):
-        _, am = model.decode(toks, pos, [table], want_logits=False)
-        ms, by = model.profile_get()
-        gemv_ms += ms[0]
-        attn_ms += ms[1]
-        other_ms += ms[2]
-        gemv_bytes += int(by[0])
-        attn_bytes += int(by[1])
-        toks = am.tolist()
-        pos = [p + 1 for p in pos]
+    toks, pos = decode_loop(model, toks, pos, [table], steps, bs)
     ctx.sync()
     elapsed = time.perf_counter() - t0
-    model.profile(False)
+    prof = profile_pass(model, toks, pos, [table], min(steps, 20))
     kv_state = model.kv_download() if os.environ.get("BENCH_CPU", "1") == "1" else None
     res = dict(tok_s=steps / elapsed, ms_per_step=1e3 * elapsed / steps, prefill_tok_s=prompt_len / prefill_s,
-               gemv_ms=gemv_ms / steps, attn_ms=attn_ms / steps, other_ms=other_ms / steps,
-               gemv_bytes=gemv_bytes / steps, attn_bytes=attn_bytes / steps, last_tok=toks[0], last_pos=pos[0],
-               table=table, nb=nb, weight_bytes=model.weight_bytes())
+               last_tok=toks[0], last_pos=pos[0], table=table, nb=nb, weight_bytes=model.weight_bytes(), **prof)
     model.close()
     return res, kv_state
 
@@ -100,7 +105,7 @@ def run_b32(ctx, cfg, weights, steps, warmup, batch=32):
     bs = 16
     rng = np.random.default_rng(SEED + 32)
     ctxs = rng.integers(128, 2049, batch)
-    need = [(int(c) + warmup + steps + 2 + bs - 1) // bs for c in ctxs]
+    need = [(int(c) + warmup + steps + 8 + bs - 1) // bs for c in ctxs]
     nb = sum(need)
     perm = rng.permutation(nb).tolist()
     tables, k = [], 0
@@ -118,28 +123,35 @@ def run_b32(ctx, cfg, weights, steps, warmup, batch=32):
     ctx.sync()
     prefill_s = time.perf_counter() - t0
     toks, pos = decode_loop(model, first, [int(c) for c in ctxs], tables, warmup, bs)
-    model.profile(True)
-    gemv_ms = attn_ms = 0.0
-    gemv_bytes = attn_bytes = 0
     ctx.sync()
     t0 = time.perf_counter()
-    for _ in range(steps):
-        _, am = model.decode(toks, pos, tables, want_logits=False)
-        ms, by = model.profile_get()
-        gemv_ms += ms[0]
-        attn_ms += ms[1]
-        gemv_bytes += int(by[0])
-        attn_bytes += int(by[1])
-        toks = am.tolist()
-        pos = [p + 1 for p in pos]
+    toks, pos = decode_loop(model, toks, pos, tables, steps, bs)
     ctx.sync()
     elapsed = time.perf_counter() - t0
+    prof = profile_pass(model, toks, pos, tables, min(steps, 5))
+    gemv_ms, attn_ms, gemv_bytes, attn_bytes = prof["gemv_ms"], prof["attn_ms"], prof["gemv_bytes"], prof["attn_bytes"]
     model.close()
     return dict(tok_s=batch * steps / elapsed, ms_per_step=1e3 * elapsed / steps,
                 prefill_tok_s=float(np.sum(ctxs)) / prefill_s, mean_ctx=float(np.mean(ctxs)),
                 gemv_gbs=(gemv_bytes / 1e9) / (gemv_ms / 1e3) if gemv_ms else None,
                 attn_gbs=(attn_bytes / 1e9) / (attn_ms / 1e3) if attn_ms else None,
-                gemv_ms=gemv_ms / steps, attn_ms=attn_ms / steps)
+                gemv_ms=gemv_ms, attn_ms=attn_ms)
+
+
+SWEEP_SHAPES = [  # (name, rows, cols) of the fused projections
+    ("tl.qkv", 2560, 2048), ("tl.o", 2048, 2048), ("tl.gate_up", 11264, 2048), ("tl.down", 2048, 5632),
+    ("tl.lm_head", 32000, 2048), ("l3.qkv", 6144, 4096), ("l3.o", 4096, 4096), ("l3.gate_up", 28672, 4096),
+    ("l3.down", 4096, 14336), ("l3.lm_head", 128256, 4096)]
+
+
+def gemv_sweep(ctx, batch=1, reps=20):
+    """Per-shape int8 projection time: `reps` launches captured in one graph, HIP events around
+    a replay (pia_bench_projection). Bytes are the algorithmic bytes of one launch."""
+    out = {}
+    for name, rows, cols in SWEEP_SHAPES:
+        us, by = pia.bench_projection(ctx, rows, cols, batch, reps)
+        out[name] = {"us": round(us, 2), "GB/s": round(by / us / 1e3, 1), "frac": round(by / us / 1e3 / HBM_PEAK_GBS, 3)}
+    return out
 
 
 def cpu_baseline(cfg, weights, b1, kv_state, budget_s=15.0):
@@ -177,6 +189,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-b32", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sweep", action="store_true", help="also time each projection shape alone")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the int8 decode path is built and measured on a single MI355X; "
@@ -218,6 +231,9 @@ def main():
         log("B=32 paged decode")
         b32 = run_b32(ctx, cfg, weights, max(5, args.steps // 4), max(2, args.warmup // 2))
         out["b32"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in b32.items()}
+    if args.sweep:
+        log("GEMV shape sweep")
+        out["gemv_sweep_b1"] = gemv_sweep(ctx, 1)
     if not args.no_cpu:
         log("CPU baseline")
         out["cpu_baseline"] = cpu_baseline(cfg, weights, b1, kv_state)

@@ -231,6 +231,17 @@ pia_status pia_model_profile(pia_model* m, int32_t enable);
 pia_status pia_model_profile_get(pia_model* m, double* ms_per_class, int64_t* bytes_per_class, int32_t n_class);
 
 /* ------------------------------------------------------------------------------------ */
+/* Diagnostics (no counterpart in the reference).                                         */
+/* ------------------------------------------------------------------------------------ */
+/* Device time of one int8 projection launch of shape rows x cols at `batch` (the kernel the
+ * model uses for that shape): `reps` launches captured in one graph, cycling through enough
+ * distinct weight copies (>= 1 GiB) that every launch streams from HBM, HIP events around a
+ * replay; *us = mean microseconds per launch. Also reports the launch's
+ * algorithmic bytes (int8 weights + scales + activations in + results out). */
+pia_status pia_bench_projection(pia_context* ctx, int64_t rows, int64_t cols, int64_t batch, int32_t reps, double* us,
+                                int64_t* bytes);
+
+/* ------------------------------------------------------------------------------------ */
 /* Synthetic inputs (no counterpart in the reference: seeded data for tests and benches). */
 /* ------------------------------------------------------------------------------------ */
 /* n samples of N(0, std^2) as f32 from (seed, stream): SplitMix64 + Box-Muller in f64. */

@@ -6,7 +6,9 @@
 // launches; rows are padded to 16 bytes (int8) so every lane issues aligned 128-bit loads.
 // Activations are [batch][ld] f32 with ld a multiple of 16 floats.
 #include <algorithm>
+#include <array>
 #include <cmath>
+#include <map>
 #include <cstring>
 #include <vector>
 
@@ -18,6 +20,9 @@ namespace pia {
 namespace {
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// Rows up to which RMSNorm is fused into the projection that consumes it.
+constexpr int64_t kFusedNormRows = 64;
 
 struct Proj {
   int kind = -1;  // -1 unset, 0 f32, 1 int8
@@ -71,7 +76,7 @@ struct pia_model {
   pia_context* ctx = nullptr;
   pia_model_config cfg{};
   int64_t hd = 0, kvd = 0, qkv_rows = 0;
-  int64_t ld_h = 0, ld_qkv = 0, ld_gu = 0, ld_i = 0, ld_v = 0;
+  int64_t ld_h = 0, ld_qkv = 0, ld_i = 0, ld_v = 0;
   DeviceBuffer embed, final_norm;
   bool embed_set = false, final_norm_set = false;
   std::vector<Layer> layers;
@@ -84,11 +89,28 @@ struct pia_model {
   int64_t rope_len = 0;
 
   int64_t cap = 0;  // rows of activation scratch
-  DeviceBuffer x, xb, qkv, attn, gu, h, logits, amax, attn_work, step;
-  PinnedBuffer pin;
+  DeviceBuffer x, xb, qkv, attn, h, logits, amax, attn_work, counters, step;
+  PinnedBuffer pin, pin_out;
   Prof prof;
 
+  // Replayable decode / prefill steps. Every kernel argument is a device pointer into the
+  // buffers above, so a graph stays valid until one of them is reallocated.
+  std::map<std::array<int64_t, 6>, hipGraphExec_t> graphs;
+
+  ~pia_model() { drop_graphs(); }
+
   hipStream_t st() const { return ctx->stream; }
+
+  void drop_graphs() {
+    for (auto& kv_ : graphs) (void)hipGraphExecDestroy(kv_.second);
+    graphs.clear();
+  }
+  void grow(DeviceBuffer& b, size_t need) {
+    if (need <= b.bytes) return;
+    PIA_HIP(hipStreamSynchronize(st()));
+    drop_graphs();
+    b.ensure(need);
+  }
 
   void begin(int cls, int64_t bytes, hipEvent_t* b) {
     if (!prof.on) return;
@@ -100,17 +122,27 @@ struct pia_model {
   void end(hipEvent_t b) {
     if (prof.on) PIA_HIP(hipEventRecord(b, st()));
   }
+  template <typename F>
+  void timed(int cls, int64_t bytes, F&& f) {
+    hipEvent_t b = nullptr;
+    begin(cls, bytes, &b);
+    f();
+    end(b);
+  }
 
   void ensure_cap(int64_t rows) {
     if (rows <= cap) return;
     const int64_t c = std::max<int64_t>(rows, 8);
-    x.ensure(c * ld_h * 4);
-    xb.ensure(c * ld_h * 4);
-    qkv.ensure(c * ld_qkv * 4);
-    attn.ensure(c * ld_h * 4);
-    gu.ensure(c * ld_gu * 4);
-    h.ensure(c * ld_i * 4);
-    amax.ensure(c * 4);
+    grow(x, c * ld_h * 4);
+    grow(xb, c * ld_h * 4);
+    grow(qkv, c * ld_qkv * 4);
+    grow(attn, c * ld_h * 4);
+    grow(h, c * ld_i * 4);
+    grow(amax, c * 8);
+    if (static_cast<size_t>(c * cfg.kv_heads * 4) > counters.bytes) {
+      grow(counters, c * cfg.kv_heads * 4);
+      PIA_HIP(hipMemset(counters.ptr, 0, counters.bytes));
+    }
     cap = c;
   }
 
@@ -130,6 +162,7 @@ struct pia_model {
       }
     }
     PIA_HIP(hipStreamSynchronize(st()));
+    drop_graphs();
     rope_cos.release();
     rope_sin.release();
     rope_cos.ensure(c.size() * 4);
@@ -139,25 +172,34 @@ struct pia_model {
     rope_len = n;
   }
 
-  int64_t proj_bytes(const Proj& p, int64_t batch) const {
+  // Algorithmic bytes of one projection launch: int8 weights + scales (or f32 weights),
+  // activations in, results out.
+  static int64_t proj_bytes(const Proj& p, int64_t batch, Epi epi) {
     const int64_t wb = p.kind == 1 ? p.rows * p.cols + 4 * p.rows : 4 * p.rows * p.cols;
-    return wb + 4 * batch * p.cols + 4 * batch * p.rows;
+    const int64_t outr = epi == Epi::Swiglu ? p.rows / 2 : p.rows;
+    return wb + 4 * batch * p.cols + 4 * batch * outr;
   }
 
-  void gemv(const Proj& p, const float* x_in, int64_t ldx, float* out, int64_t ldo, int64_t batch, Epi epi) {
+  void gemv(const Proj& p, const float* x_in, int64_t ldx, const float* norm_w, float* out, int64_t ldo,
+            int64_t batch, Epi epi, unsigned long long* amax_out = nullptr) {
     hipEvent_t b = nullptr;
-    begin(0, proj_bytes(p, batch), &b);
-    launch_gemv(p.kind, p.w.ptr, p.ld, p.kind == 1 ? p.s.as<float>() : nullptr, x_in, ldx, out, ldo, 1, p.rows, p.cols,
-                batch, epi, st());
+    begin(0, proj_bytes(p, batch, epi), &b);
+    GemvArgs g{p.kind, p.w.ptr, p.ld, p.kind == 1 ? p.s.as<float>() : nullptr, x_in, ldx, norm_w, cfg.rms_eps,
+               out, ldo, 1, p.rows, p.cols, batch, epi, amax_out};
+    launch_gemv(g, st());
     end(b);
   }
 
-  template <typename F>
-  void timed(int cls, int64_t bytes, F&& f) {
-    hipEvent_t b = nullptr;
-    begin(cls, bytes, &b);
-    f();
-    end(b);
+  // A projection whose input is RMSNorm(x) * w: fused into the projection for small batches,
+  // a separate normalization pass into xb for large ones.
+  void normed_gemv(const Proj& p, const float* X, const float* norm_w, int64_t n, float* out, int64_t ldo, Epi epi,
+                   unsigned long long* amax_out = nullptr) {
+    if (n <= kFusedNormRows) {
+      gemv(p, X, ld_h, norm_w, out, ldo, n, epi, amax_out);
+    } else {
+      timed(2, 0, [&] { launch_rmsnorm(X, ld_h, norm_w, xb.as<float>(), ld_h, n, cfg.hidden, cfg.rms_eps, st()); });
+      gemv(p, xb.as<float>(), ld_h, nullptr, out, ldo, n, epi, amax_out);
+    }
   }
 
   void check_complete() const {
@@ -171,41 +213,49 @@ struct pia_model {
     PIA_REQUIRE(kv.ptr != nullptr, "model: KV cache not allocated (pia_model_kv_alloc)");
   }
 
-  // run_layers_batch (src/model.rs:968-1177) for `batch` rows whose step inputs are already on
-  // the device. Leaves the final normalized hidden state in xb.
-  void run_layers(int64_t batch, const int32_t* d_tokens, const pia_attn_entry* d_entries, const int32_t* d_tables,
-                  int64_t max_window, int64_t mapped_tokens) {
+  struct StepDev {
+    const int32_t* tokens;
+    const pia_attn_entry* entries;
+    const int32_t* tables;
+  };
+
+  // run_layers_batch (src/model.rs:968-1177) for `n` rows whose step inputs are already on the
+  // device; leaves the residual stream (before the final norm) in x.
+  void run_layers(int64_t n, const StepDev& in, const AttnPlan& plan, bool fused, int64_t mapped_tokens) {
     const auto& c = cfg;
-    const int64_t splits = attention_splits(std::max<int64_t>(1, max_window));
-    const int64_t wb = attention_work_bytes(batch, c.heads, hd, splits);
-    if (wb) attn_work.ensure(wb);
-    const int64_t attn_bytes = mapped_tokens * c.kv_heads * 2 * hd * 4 + 2 * batch * c.hidden * 4;
+    const int64_t attn_bytes = mapped_tokens * c.kv_heads * 2 * hd * 4 + 2 * n * c.hidden * 4;
     float* X = x.as<float>();
-    float* XB = xb.as<float>();
     float* QKV = qkv.as<float>();
     float* ATT = attn.as<float>();
-    float* GU = gu.as<float>();
     float* H = h.as<float>();
-    timed(2, 0, [&] { launch_embed(d_tokens, embed.as<uint16_t>(), X, ld_h, batch, c.hidden, c.vocab, st()); });
+    timed(2, 0, [&] {
+      launch_embed(in.tokens, embed.as<uint16_t>(), X, ld_h, n, c.hidden, c.vocab, amax.as<unsigned long long>(), st());
+    });
     for (int64_t l = 0; l < c.layers; ++l) {
       Layer& L = layers[l];
-      timed(2, 0, [&] { launch_rmsnorm(X, ld_h, L.attn_norm.as<float>(), XB, ld_h, batch, c.hidden, c.rms_eps, st()); });
-      gemv(L.qkv, XB, ld_h, QKV, ld_qkv, batch, Epi::Store);
-      timed(2, 0, [&] {
-        launch_rope_kv_write(QKV, ld_qkv, d_entries, d_tables, rope_cos.as<float>(), rope_sin.as<float>(),
-                             kv.as<float>(), layout, c.heads, batch, l, st());
-      });
+      normed_gemv(L.qkv, X, L.attn_norm.as<float>(), n, QKV, ld_qkv, Epi::Store);
       timed(1, attn_bytes, [&] {
-        launch_attention(QKV, ld_qkv, ATT, ld_h, kv.as<float>(), layout, c.heads, d_entries, d_tables, batch, l, splits,
-                         attn_work.ptr, st());
+        if (!fused)
+          launch_rope_kv_write(QKV, ld_qkv, in.entries, in.tables, rope_cos.as<float>(), rope_sin.as<float>(),
+                               kv.as<float>(), layout, c.heads, n, l, st());
+        AttnLaunch a{QKV, ld_qkv, ATT, ld_h, kv.as<float>(), &layout, c.heads, in.entries, in.tables, n, l, plan,
+                     attn_work.ptr, counters.as<int>(), fused, rope_cos.as<float>(), rope_sin.as<float>()};
+        launch_attention(a, st());
       });
-      gemv(L.o, ATT, ld_h, X, ld_h, batch, Epi::Add);
-      timed(2, 0, [&] { launch_rmsnorm(X, ld_h, L.ffn_norm.as<float>(), XB, ld_h, batch, c.hidden, c.rms_eps, st()); });
-      gemv(L.gu, XB, ld_h, GU, ld_gu, batch, Epi::Store);
-      timed(2, 0, [&] { launch_swiglu(GU, ld_gu, H, ld_i, batch, c.inter, st()); });
-      gemv(L.down, H, ld_i, X, ld_h, batch, Epi::Add);
+      gemv(L.o, ATT, ld_h, nullptr, X, ld_h, n, Epi::Add);
+      normed_gemv(L.gu, X, L.ffn_norm.as<float>(), n, H, ld_i, Epi::Swiglu);
+      gemv(L.down, H, ld_i, nullptr, X, ld_h, n, Epi::Add);
     }
-    timed(2, 0, [&] { launch_rmsnorm(X, ld_h, final_norm.as<float>(), XB, ld_h, batch, c.hidden, c.rms_eps, st()); });
+  }
+
+  // Copy the fused-argmax slots back (the low 32 bits are the row) and wait for the step.
+  void read_argmax(int32_t* out, int64_t batch) {
+    pin_out.ensure(batch * 8);
+    PIA_HIP(hipMemcpyAsync(pin_out.ptr, amax.ptr, batch * 8, hipMemcpyDeviceToHost, st()));
+    PIA_HIP(hipStreamSynchronize(st()));
+    const auto* v = static_cast<const unsigned long long*>(pin_out.ptr);
+    if (out)
+      for (int64_t b = 0; b < batch; ++b) out[b] = static_cast<int32_t>(v[b] & 0xffffffffull);
   }
 
   void finish_prof() {
@@ -219,6 +269,37 @@ struct pia_model {
       prof.bytes[r.cls] += r.bytes;
     }
     prof.reset();
+  }
+
+  // Run `body` eagerly (profiling: a short device spin first lets the host enqueue ahead, so
+  // each kernel's events bracket only that kernel), or through a cached graph for `key`.
+  template <typename F>
+  void run_step(const std::array<int64_t, 6>& key, F&& body) {
+    if (prof.on) {
+      prof.reset();
+      launch_spin(3000.0, st());
+      body();
+      return;
+    }
+    auto it = graphs.find(key);
+    if (it == graphs.end()) {
+      hipGraph_t g = nullptr;
+      PIA_HIP(hipStreamBeginCapture(st(), hipStreamCaptureModeRelaxed));
+      try {
+        body();
+      } catch (...) {
+        (void)hipStreamEndCapture(st(), &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      PIA_HIP(hipStreamEndCapture(st(), &g));
+      hipGraphExec_t exec = nullptr;
+      const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      PIA_HIP(e);
+      it = graphs.emplace(key, exec).first;
+    }
+    PIA_HIP(hipGraphLaunch(it->second, st()));
   }
 };
 
@@ -236,18 +317,20 @@ void alloc_proj(Proj& p, int kind, int64_t rows, int64_t cols) {
   p.filled = 0;
 }
 
-// Copy `rows` host rows of `cols` into p at row offset r0, with row padding.
-void upload_rows(Proj& p, int64_t r0, int64_t rows, const void* src, const float* scales) {
+// Copy `rows` host rows of `cols` into p at device rows r0, r0 + step, ..., with row padding.
+void upload_rows(Proj& p, int64_t r0, int64_t rows, int64_t step, const void* src, const float* scales) {
   const int64_t esz = p.kind == 1 ? 1 : 4;
-  PIA_HIP(hipMemcpy2D(static_cast<char*>(p.w.ptr) + r0 * p.ld * esz, p.ld * esz, src, p.cols * esz, p.cols * esz, rows,
-                      hipMemcpyHostToDevice));
-  if (p.kind == 1) PIA_HIP(hipMemcpy(p.s.as<float>() + r0, scales, rows * 4, hipMemcpyHostToDevice));
+  PIA_HIP(hipMemcpy2D(static_cast<char*>(p.w.ptr) + r0 * p.ld * esz, step * p.ld * esz, src, p.cols * esz,
+                      p.cols * esz, rows, hipMemcpyHostToDevice));
+  if (p.kind == 1)
+    PIA_HIP(hipMemcpy2D(p.s.as<float>() + r0, step * 4, scales, 4, 4, rows, hipMemcpyHostToDevice));
 }
 
 struct Target {
   Proj* p;
   int64_t r0, rows, cols;
   uint32_t bit;
+  int64_t row_step = 1;  // device rows between consecutive source rows
 };
 
 Target target_of(pia_model* m, int64_t layer, int32_t which) {
@@ -260,8 +343,9 @@ Target target_of(pia_model* m, int64_t layer, int32_t which) {
     case PIA_WK: return {&L.qkv, c.hidden, m->kvd, c.hidden, 2};
     case PIA_WV: return {&L.qkv, c.hidden + m->kvd, m->kvd, c.hidden, 4};
     case PIA_WO: return {&L.o, 0, c.hidden, c.hidden, 1};
-    case PIA_W1: return {&L.gu, 0, c.inter, c.hidden, 1};
-    case PIA_W3: return {&L.gu, c.inter, c.inter, c.hidden, 2};
+    // gate / up rows interleaved: row 2i = gate i, row 2i + 1 = up i (SwiGLU epilogue).
+    case PIA_W1: return {&L.gu, 0, c.inter, c.hidden, 1, 2};
+    case PIA_W3: return {&L.gu, 1, c.inter, c.hidden, 2, 2};
     case PIA_W2: return {&L.down, 0, c.hidden, c.inter, 1};
     default: fail(PIA_ERR_INVALID, "unknown projection slot");
   }
@@ -289,7 +373,7 @@ void set_proj(pia_model* m, int64_t layer, int32_t which, int kind, const void* 
                 "fused projection group mixes int8 and f32 slots; set every slot of the group with one kind");
     alloc_proj(*t.p, kind, total_rows(m, t.p), t.cols);
   }
-  upload_rows(*t.p, t.r0, t.rows, data, scales);
+  upload_rows(*t.p, t.r0, t.rows, t.row_step, data, scales);
   t.p->filled |= t.bit;
 }
 
@@ -313,7 +397,6 @@ pia_status pia_model_create(pia_context* ctx, const pia_model_config* cfg, pia_m
   m->qkv_rows = c.hidden + 2 * m->kvd;
   m->ld_h = round_up(c.hidden, 16);
   m->ld_qkv = round_up(m->qkv_rows, 16);
-  m->ld_gu = round_up(2 * c.inter, 16);
   m->ld_i = round_up(c.inter, 16);
   m->ld_v = round_up(c.vocab, 16);
   m->layers.resize(c.layers);
@@ -428,21 +511,16 @@ int64_t window_start(int64_t pos, int64_t window) {
   return pos + 1 > window ? pos + 1 - window : 0;
 }
 
-// Stage tokens, entries and tables in one pinned buffer and one host->device copy.
-struct StepInputs {
-  const int32_t* tokens;
-  const pia_attn_entry* entries;
-  const int32_t* tables;
-};
-
-StepInputs upload_step(pia_model* m, const std::vector<int32_t>& tok, const std::vector<pia_attn_entry>& ent,
-                       const int32_t* tables, int64_t ntab) {
+// Stage tokens, entries and tables in one pinned buffer and one host->device copy. The
+// device step buffer keeps its address across calls (captured graphs read it).
+pia_model::StepDev upload_step(pia_model* m, const std::vector<int32_t>& tok, const std::vector<pia_attn_entry>& ent,
+                               const int32_t* tables, int64_t ntab) {
   const size_t n = tok.size();
-  const size_t off_e = round_up(n * 4, 64), off_t = off_e + round_up(n * sizeof(pia_attn_entry), 64);
-  const size_t total = off_t + round_up(std::max<int64_t>(ntab, 1) * 4, 64);
+  const size_t off_e = round_up(n * 4, 256), off_t = off_e + round_up(n * sizeof(pia_attn_entry), 256);
+  const size_t total = off_t + round_up(std::max<int64_t>(ntab, 1) * 4, 256);
   PIA_HIP(hipStreamSynchronize(m->st()));  // the pinned staging buffer may still be in flight
   m->pin.ensure(total);
-  m->step.ensure(total);
+  m->grow(m->step, std::max<size_t>(total, 1 << 16));
   char* p = static_cast<char*>(m->pin.ptr);
   std::memcpy(p, tok.data(), n * 4);
   std::memcpy(p + off_e, ent.data(), n * sizeof(pia_attn_entry));
@@ -457,6 +535,29 @@ int64_t mapped_in_window(const pia_attn_entry& e, int64_t bs) {
   // Tokens of start..=pos that fall inside mapped logical blocks (the K/V actually read).
   const int64_t end = std::min<int64_t>(e.pos + 1, static_cast<int64_t>(e.table_len) * bs);
   return std::max<int64_t>(0, end - e.start);
+}
+
+// The fused attention writes each entry's K/V inside the attention launch, so it is only
+// used when no entry can read a slot another entry of the batch writes: the block each entry
+// writes must appear in no other entry's table (always true for decode batches after
+// copy-on-write; never for prefill chunks, whose entries share one table).
+bool fusable(const std::vector<pia_attn_entry>& ent, const int32_t* tables, int64_t bs, int64_t window) {
+  if (window == 0) return false;  // the K/V write must still happen with an empty window
+  std::map<int32_t, int> owner;   // written block -> entry
+  for (size_t b = 0; b < ent.size(); ++b) {
+    const int64_t lb = ent[b].pos / bs;
+    if (lb < ent[b].table_len) {
+      const int32_t blk = tables[ent[b].table_off + lb];
+      if (!owner.emplace(blk, static_cast<int>(b)).second) return false;
+    }
+  }
+  if (owner.empty()) return true;
+  for (size_t b = 0; b < ent.size(); ++b)
+    for (int32_t i = 0; i < ent[b].table_len; ++i) {
+      auto it = owner.find(tables[ent[b].table_off + i]);
+      if (it != owner.end() && it->second != static_cast<int>(b)) return false;
+    }
+  return true;
 }
 
 }  // namespace
@@ -477,7 +578,8 @@ pia_status pia_model_decode(pia_model* m, const uint32_t* tokens, const int64_t*
   std::vector<pia_attn_entry> ent(batch);
   for (int64_t b = 0; b < batch; ++b) {
     PIA_REQUIRE(positions[b] >= 0 && positions[b] < (int64_t(1) << 30), "position out of range");
-    PIA_REQUIRE(table_off[b] >= 0 && table_len[b] >= 0, "negative table offset/length");
+    PIA_REQUIRE(table_off[b] >= 0 && table_len[b] >= 0 && table_off[b] + table_len[b] < (int64_t(1) << 31),
+                "bad table offset/length");
     ntab = std::max(ntab, table_off[b] + table_len[b]);
     max_pos = std::max(max_pos, positions[b]);
     tok[b] = static_cast<int32_t>(tokens[b]);
@@ -490,19 +592,23 @@ pia_status pia_model_decode(pia_model* m, const uint32_t* tokens, const int64_t*
   PIA_REQUIRE(ntab == 0 || tables, "null block tables");
   for (int64_t i = 0; i < ntab; ++i)
     PIA_REQUIRE(tables[i] >= 0 && tables[i] < m->layout.num_blocks, "block table entry out of range");
+  const AttnPlan plan = plan_attention(batch, c.kv_heads, m->hd, max_window, m->ctx->num_cus);
+  const bool fused = fusable(ent, tables, m->layout.block_size, c.attention_window);
   m->ensure_cap(batch);
   m->ensure_rope(max_pos);
-  m->logits.ensure(batch * m->ld_v * 4);
-  StepInputs in = upload_step(m, tok, ent, tables, ntab);
-  m->prof.reset();
-  m->run_layers(batch, in.tokens, in.entries, in.tables, max_window, mapped);
-  m->gemv(m->lm_head, m->xb.as<float>(), m->ld_h, m->logits.as<float>(), m->ld_v, batch, Epi::Store);
-  m->timed(2, 0, [&] { launch_argmax(m->logits.as<float>(), m->ld_v, m->amax.as<int32_t>(), batch, c.vocab, m->st()); });
+  m->grow(m->logits, batch * m->ld_v * 4);
+  const int64_t wb = attention_work_bytes(batch, c.heads, m->hd, plan.splits);
+  if (wb) m->grow(m->attn_work, wb);
+  const pia_model::StepDev in = upload_step(m, tok, ent, tables, ntab);
+  m->run_step({0, batch, plan.split, plan.splits, fused ? 1 : 0, 0}, [&] {
+    m->run_layers(batch, in, plan, fused, mapped);
+    m->normed_gemv(m->lm_head, m->x.as<float>(), m->final_norm.as<float>(), batch, m->logits.as<float>(), m->ld_v,
+                   Epi::Store, m->amax.as<unsigned long long>());
+  });
   if (logits)
     PIA_HIP(hipMemcpy2DAsync(logits, c.vocab * 4, m->logits.ptr, m->ld_v * 4, c.vocab * 4, batch,
                              hipMemcpyDeviceToHost, m->st()));
-  if (argmax) PIA_HIP(hipMemcpyAsync(argmax, m->amax.ptr, batch * 4, hipMemcpyDeviceToHost, m->st()));
-  PIA_HIP(hipStreamSynchronize(m->st()));
+  m->read_argmax(argmax, batch);
   m->finish_prof();
   PIA_API_END
 }
@@ -513,7 +619,7 @@ pia_status pia_model_prefill(pia_model* m, const uint32_t* tokens, int64_t n, in
   PIA_REQUIRE(m && tokens, "null argument");
   PIA_REQUIRE(n > 0, "prefill needs at least one token");
   PIA_REQUIRE(start_pos >= 0 && start_pos + n < (int64_t(1) << 30), "position out of range");
-  PIA_REQUIRE(table_len >= 0 && (table_len == 0 || table), "bad block table");
+  PIA_REQUIRE(table_len >= 0 && table_len < (int64_t(1) << 31) && (table_len == 0 || table), "bad block table");
   m->check_complete();
   PIA_HIP(hipSetDevice(m->ctx->device));
   const auto& c = m->cfg;
@@ -530,18 +636,22 @@ pia_status pia_model_prefill(pia_model* m, const uint32_t* tokens, int64_t n, in
     max_window = std::max(max_window, pos + 1 - st);
     mapped += mapped_in_window(ent[i], m->layout.block_size);
   }
+  const AttnPlan plan = plan_attention(n, c.kv_heads, m->hd, max_window, m->ctx->num_cus);
+  const bool fused = n == 1 && fusable(ent, table, m->layout.block_size, c.attention_window);
   m->ensure_cap(n);
   m->ensure_rope(start_pos + n);
-  m->logits.ensure(m->ld_v * 4);
-  StepInputs in = upload_step(m, tok, ent, table, table_len);
-  m->prof.reset();
-  m->run_layers(n, in.tokens, in.entries, in.tables, max_window, mapped);
-  // Only the last position pays for the LM head (src/model.rs:1249-1254).
-  m->gemv(m->lm_head, m->xb.as<float>() + (n - 1) * m->ld_h, m->ld_h, m->logits.as<float>(), m->ld_v, 1, Epi::Store);
-  m->timed(2, 0, [&] { launch_argmax(m->logits.as<float>(), m->ld_v, m->amax.as<int32_t>(), 1, c.vocab, m->st()); });
+  m->grow(m->logits, m->ld_v * 4);
+  const int64_t wb = attention_work_bytes(n, c.heads, m->hd, plan.splits);
+  if (wb) m->grow(m->attn_work, wb);
+  const pia_model::StepDev in = upload_step(m, tok, ent, table, table_len);
+  m->run_step({1, n, plan.split, plan.splits, fused ? 1 : 0, 0}, [&] {
+    m->run_layers(n, in, plan, fused, mapped);
+    // Only the last position pays for the LM head (src/model.rs:1249-1254).
+    m->normed_gemv(m->lm_head, m->x.as<float>() + (n - 1) * m->ld_h, m->final_norm.as<float>(), 1,
+                   m->logits.as<float>(), m->ld_v, Epi::Store, m->amax.as<unsigned long long>());
+  });
   if (logits) PIA_HIP(hipMemcpyAsync(logits, m->logits.ptr, c.vocab * 4, hipMemcpyDeviceToHost, m->st()));
-  if (argmax) PIA_HIP(hipMemcpyAsync(argmax, m->amax.ptr, 4, hipMemcpyDeviceToHost, m->st()));
-  PIA_HIP(hipStreamSynchronize(m->st()));
+  m->read_argmax(argmax, 1);
   m->finish_prof();
   PIA_API_END
 }

@@ -1,6 +1,7 @@
 // Context, device-memory helpers and the kernel-tier C ABI (src/math.rs, src/attention.rs,
 // src/memory/layout.rs seams), plus the synthetic-input helpers.
 #include <cmath>
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -189,7 +190,8 @@ pia_status pia_matvec_i8_dev(pia_context* ctx, float* out, const float* x, const
                              int64_t rows, int64_t cols, void* stream) {
   PIA_API_BEGIN
   PIA_REQUIRE(ctx && out && x && w && scales, "null argument");
-  launch_gemv(1, w, cols, scales, x, cols, out, 0, 1, rows, cols, 1, Epi::Store, stream_of(ctx, stream));
+  launch_gemv(GemvArgs{1, w, cols, scales, x, cols, nullptr, 0.f, out, 0, 1, rows, cols, 1, Epi::Store},
+              stream_of(ctx, stream));
   PIA_API_END
 }
 
@@ -197,7 +199,8 @@ pia_status pia_matmat_i8_dev(pia_context* ctx, float* out_rb, const float* x_br,
                              const float* scales, int64_t batch, int64_t rows, int64_t cols, void* stream) {
   PIA_API_BEGIN
   PIA_REQUIRE(ctx && out_rb && x_br && w && scales, "null argument");
-  launch_gemv(1, w, cols, scales, x_br, cols, out_rb, 1, batch, rows, cols, batch, Epi::Store, stream_of(ctx, stream));
+  launch_gemv(GemvArgs{1, w, cols, scales, x_br, cols, nullptr, 0.f, out_rb, 1, batch, rows, cols, batch, Epi::Store},
+              stream_of(ctx, stream));
   PIA_API_END
 }
 
@@ -205,7 +208,8 @@ pia_status pia_qlinear_apply_dev(pia_context* ctx, float* out_br, const float* x
                                  const float* scales, int64_t batch, int64_t rows, int64_t cols, void* stream) {
   PIA_API_BEGIN
   PIA_REQUIRE(ctx && out_br && x_br && w && scales, "null argument");
-  launch_gemv(1, w, cols, scales, x_br, cols, out_br, rows, 1, rows, cols, batch, Epi::Store, stream_of(ctx, stream));
+  launch_gemv(GemvArgs{1, w, cols, scales, x_br, cols, nullptr, 0.f, out_br, rows, 1, rows, cols, batch, Epi::Store},
+              stream_of(ctx, stream));
   PIA_API_END
 }
 
@@ -229,8 +233,9 @@ pia_status pia_matmat_i8(pia_context* ctx, float* out_rb, const float* x_br, con
   PIA_HIP(hipMemcpyAsync(dw.ptr, w, rows * cols, hipMemcpyHostToDevice, st));
   PIA_HIP(hipMemcpyAsync(ds.ptr, scales, rows * sizeof(float), hipMemcpyHostToDevice, st));
   PIA_HIP(hipMemcpyAsync(dx.ptr, x_br, batch * cols * sizeof(float), hipMemcpyHostToDevice, st));
-  launch_gemv(1, dw.ptr, cols, static_cast<const float*>(ds.ptr), static_cast<const float*>(dx.ptr), cols,
-              static_cast<float*>(dout.ptr), 1, batch, rows, cols, batch, Epi::Store, st);
+  launch_gemv(GemvArgs{1, dw.ptr, cols, static_cast<const float*>(ds.ptr), static_cast<const float*>(dx.ptr), cols,
+                       nullptr, 0.f, static_cast<float*>(dout.ptr), 1, batch, rows, cols, batch, Epi::Store},
+              st);
   PIA_HIP(hipMemcpyAsync(out_rb, dout.ptr, batch * rows * sizeof(float), hipMemcpyDeviceToHost, st));
   PIA_HIP(hipStreamSynchronize(st));
   PIA_API_END
@@ -258,12 +263,17 @@ pia_status pia_paged_attention_dev(pia_context* ctx, float* out, const float* q,
     widest = std::max<int64_t>(widest, e.pos + 1 - e.start);
   }
   const int64_t hd = layout->head_dim;
-  const int64_t splits = attention_splits(widest);
-  DeviceBuffer work;
-  const int64_t wb = attention_work_bytes(n, num_heads, hd, splits);
-  if (wb) work.ensure(wb);
-  launch_attention(q, num_heads * hd, out, num_heads * hd, kv, *layout, num_heads, entries, tables, n, layer, splits,
-                   work.ptr, st);
+  const AttnPlan plan = plan_attention(n, layout->num_kv_heads, hd, widest, ctx->num_cus);
+  DeviceBuffer work, counters;
+  const int64_t wb = attention_work_bytes(n, num_heads, hd, plan.splits);
+  if (wb) {
+    work.ensure(wb);
+    counters.ensure(n * layout->num_kv_heads * sizeof(int));
+    PIA_HIP(hipMemsetAsync(counters.ptr, 0, counters.bytes, st));
+  }
+  AttnLaunch a{q, num_heads * hd, out, num_heads * hd, const_cast<float*>(kv), layout, num_heads, entries, tables,
+               n, layer, plan, work.ptr, counters.as<int>(), false, nullptr, nullptr};
+  launch_attention(a, st);
   PIA_HIP(hipStreamSynchronize(st));
   PIA_API_END
 }
@@ -282,6 +292,63 @@ pia_status pia_argmax_dev(pia_context* ctx, int32_t* out, const float* logits, i
   PIA_REQUIRE(ctx && out && logits, "null argument");
   PIA_REQUIRE(vocab > 0, "empty vocabulary");
   launch_argmax(logits, vocab, out, n, vocab, stream_of(ctx, stream));
+  PIA_API_END
+}
+
+pia_status pia_bench_projection(pia_context* ctx, int64_t rows, int64_t cols, int64_t batch, int32_t reps, double* us,
+                                int64_t* bytes) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx && us && bytes, "null argument");
+  PIA_REQUIRE(rows > 0 && cols > 0 && batch > 0 && reps > 0 && reps <= 1000, "bad benchmark shape");
+  PIA_HIP(hipSetDevice(ctx->device));
+  const int64_t ldw = (cols + 15) / 16 * 16, ldx = (cols + 15) / 16 * 16;
+  // Enough distinct weight copies (>= 1 GiB in total) that consecutive launches stream from
+  // HBM instead of hitting the 256 MB Infinity Cache.
+  const int64_t wbytes = rows * ldw;
+  const int ncopy = static_cast<int>(std::min<int64_t>(64, std::max<int64_t>(2, ((int64_t(1) << 30) + wbytes - 1) / wbytes)));
+  DeviceBuffer w, s, x, y;
+  w.ensure(wbytes * ncopy);
+  s.ensure(rows * 4);
+  x.ensure(batch * ldx * 4);
+  y.ensure(batch * rows * 4);
+  {
+    std::vector<int8_t> hw(wbytes);
+    for (size_t i = 0; i < hw.size(); ++i) hw[i] = static_cast<int8_t>((i * 2654435761u >> 13) % 255 - 127);
+    for (int c = 0; c < ncopy; ++c)
+      PIA_HIP(hipMemcpy(static_cast<int8_t*>(w.ptr) + c * wbytes, hw.data(), hw.size(), hipMemcpyHostToDevice));
+    std::vector<float> hs(rows, 0.01f), hx(batch * ldx);
+    for (size_t i = 0; i < hx.size(); ++i) hx[i] = static_cast<float>((i * 40503u) % 2001) / 1000.0f - 1.0f;
+    PIA_HIP(hipMemcpy(s.ptr, hs.data(), hs.size() * 4, hipMemcpyHostToDevice));
+    PIA_HIP(hipMemcpy(x.ptr, hx.data(), hx.size() * 4, hipMemcpyHostToDevice));
+  }
+  auto args = [&](int i) {
+    return GemvArgs{1, static_cast<int8_t*>(w.ptr) + (i % ncopy) * wbytes, ldw, s.as<float>(), x.as<float>(), ldx,
+                    nullptr, 0.f, y.as<float>(), rows, 1, rows, cols, batch, Epi::Store};
+  };
+  hipStream_t st = ctx->stream;
+  launch_gemv(args(0), st);
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  PIA_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
+  for (int i = 0; i < reps; ++i) launch_gemv(args(i + 1), st);
+  PIA_HIP(hipStreamEndCapture(st, &graph));
+  PIA_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+  hipEvent_t e0, e1;
+  PIA_HIP(hipEventCreate(&e0));
+  PIA_HIP(hipEventCreate(&e1));
+  PIA_HIP(hipGraphLaunch(exec, st));
+  PIA_HIP(hipEventRecord(e0, st));
+  PIA_HIP(hipGraphLaunch(exec, st));
+  PIA_HIP(hipEventRecord(e1, st));
+  PIA_HIP(hipStreamSynchronize(st));
+  float ms = 0;
+  PIA_HIP(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  (void)hipGraphExecDestroy(exec);
+  (void)hipGraphDestroy(graph);
+  *us = 1e3 * ms / reps;
+  *bytes = rows * cols + 4 * rows + 4 * batch * cols + 4 * batch * rows;
   PIA_API_END
 }
 

@@ -11,14 +11,33 @@
 
 namespace pia {
 
-// Epilogue of a projection: store, or accumulate into the destination (residual add, as
-// src/model.rs:1127-1129 and :1165-1167 do with proj_out / ff_down).
-enum class Epi : int { Store = 0, Add = 1 };
+// Epilogue of a projection: store, accumulate into the destination (residual add, as
+// src/model.rs:1127-1129 and :1165-1167 do with proj_out / ff_down), or SwiGLU over
+// interleaved gate/up row pairs (src/math.rs:293-302).
+enum class Epi : int { Store = 0, Add = 1, Swiglu = 2 };
 
-// out[b*osb + r*osr] (=|+=) dot(W[r, :cols], x[b*ldx + :cols]) * (scales ? scales[r] : 1).
+// y[b][r] = dot(W[r, :cols], xn[b]) * (scales ? scales[r] : 1), xn = x or RMSNorm(x) * norm_w
+// when norm_w is set; written to out[b*osb + r*osr] (Store), added to it (Add), or for
+// Swiglu out[b*osb + (r/2)*osr] = silu(y[b][r]) * y[b][r+1] for even r.
 // W is int8 (wkind 1, scales required) or f32 (wkind 0), row stride ldw elements.
-void launch_gemv(int wkind, const void* W, int64_t ldw, const float* scales, const float* x, int64_t ldx, float* out,
-                 int64_t osb, int64_t osr, int64_t rows, int64_t cols, int64_t batch, Epi epi, hipStream_t st);
+struct GemvArgs {
+  int wkind;
+  const void* W;
+  int64_t ldw;
+  const float* scales;
+  const float* x;
+  int64_t ldx;
+  const float* norm_w;
+  float eps;
+  float* out;
+  int64_t osb, osr;
+  int64_t rows, cols, batch;
+  Epi epi;
+  // Optional fused greedy argmax (Store only): amax[b] = max over rows of
+  // (f32 total-order key of out[b][r]) << 32 | r; the caller zeroes amax first.
+  unsigned long long* amax = nullptr;
+};
+void launch_gemv(const GemvArgs& args, hipStream_t st);
 
 // Batched int8 projection on MFMA for batch >= 16 (decode batches and prefill).
 // Activations are split into three signed 8-bit digits per row (exact for the 23-bit
@@ -34,8 +53,9 @@ void launch_rmsnorm(const float* x, int64_t ldx, const float* w, float* out, int
                     float eps, hipStream_t st);
 
 // x[b] = bf16 embedding row (tokens[b] % vocab) widened to f32 (src/model.rs:1015-1020).
+// Also zeroes amax[0..batch) (the fused-argmax slots of this step) when amax is given.
 void launch_embed(const int32_t* tokens, const uint16_t* embed, float* x, int64_t ldx, int64_t batch, int64_t hidden,
-                  int64_t vocab, hipStream_t st);
+                  int64_t vocab, unsigned long long* amax, hipStream_t st);
 
 // NeoX RoPE on q (num_heads) and k (num_kv_heads) in place inside qkv rows (stride ldq; q at
 // column 0, k at heads*hd, v at (heads+kv_heads)*hd), then K/V scatter into the paged cache
@@ -44,13 +64,40 @@ void launch_rope_kv_write(float* qkv, int64_t ldq, const pia_attn_entry* entries
                           const float* rope_cos, const float* rope_sin, float* kv, const pia_kv_layout& layout,
                           int64_t heads, int64_t batch, int64_t layer, hipStream_t st);
 
-// PagedAttention::run for one layer. q rows have stride ldq, out rows stride ldo.
-// `work` must hold attention_work_bytes(...) bytes when more than one split is used.
-int64_t attention_splits(int64_t max_window);
+// PagedAttention::run for one layer (see attention.hip). `plan` picks the token split;
+// `work` (attention_work_bytes) and `counters` (n * num_kv_heads ints, zero between launches)
+// are needed when plan.splits > 1. When `fused`, q rows are the raw qkv rows (RoPE applied in
+// the kernel) and each entry's own K/V is rotated and written by the kernel; only valid when
+// no entry reads a cache slot written by another entry of the same launch.
+struct AttnPlan {
+  int64_t split;   // tokens per workgroup: 256, 128 or 64
+  int64_t splits;  // workgroups per (entry, kv head)
+};
+AttnPlan plan_attention(int64_t n, int64_t num_kv_heads, int64_t head_dim, int64_t max_window, int num_cus);
 int64_t attention_work_bytes(int64_t n, int64_t heads, int64_t head_dim, int64_t splits);
-void launch_attention(const float* q, int64_t ldq, float* out, int64_t ldo, const float* kv,
-                      const pia_kv_layout& layout, int64_t heads, const pia_attn_entry* entries,
-                      const int32_t* tables, int64_t n, int64_t layer, int64_t splits, void* work, hipStream_t st);
+struct AttnLaunch {
+  const float* q;
+  int64_t ldq;
+  float* out;
+  int64_t ldo;
+  float* kv;
+  const pia_kv_layout* layout;
+  int64_t heads;
+  const pia_attn_entry* entries;
+  const int32_t* tables;
+  int64_t n, layer;
+  AttnPlan plan;
+  void* work;
+  int* counters;
+  bool fused;
+  const float* rope_cos;
+  const float* rope_sin;
+};
+void launch_attention(const AttnLaunch& a, hipStream_t st);
+
+// Spin for about `us` microseconds (one thread; bounded by the device clock). Used only to let
+// the host enqueue ahead of the device while per-kernel events are being recorded.
+void launch_spin(double us, hipStream_t st);
 
 // h[b][i] = silu(gu[b][i]) * gu[b][inter + i]  (src/math.rs:293-302).
 void launch_swiglu(const float* gu, int64_t ldgu, float* h, int64_t ldh, int64_t batch, int64_t inter,

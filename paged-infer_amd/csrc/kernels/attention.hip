@@ -4,10 +4,15 @@
 // heads that share a kv head are handled together, so every K and V vector is read from HBM
 // once per entry and used for all G heads (the reference's grouped lanes,
 // src/attention.rs:12-21). The block table is resolved once per token into LDS and
-// unmapped logical blocks score -inf (src/attention.rs:233-240). Long windows are split
-// along the token axis; each split keeps its running max and sum and a second kernel
-// combines them (log-sum-exp), which is exact algebra of the reference's full-window
-// softmax with a different rounding order.
+// unmapped logical blocks score -inf (src/attention.rs:233-240). The window is split along
+// the token axis so that short batches still fill the chip; each split keeps its max and
+// sum, and the last split of an (entry, kv head) to finish combines them (log-sum-exp). That
+// is exact algebra of the reference's full-window softmax with a different rounding order.
+//
+// FUSED variant (decode batches whose entries never read a slot another entry writes): the
+// workgroup also applies NeoX RoPE to its q heads and, in the split holding the entry's own
+// position, rotates k, writes k and v into the cache and uses them straight from LDS
+// (src/model.rs:1068-1107 then :1111-1118), so a decode layer's attention is one launch.
 #include <cfloat>
 
 #include "common.h"
@@ -30,65 +35,148 @@ __device__ inline float wave_sum(float v) {
   return v;
 }
 
-template <int G>
-__global__ __launch_bounds__(kThreads) void k_attn(const float* __restrict__ q, int64_t ldq, float* __restrict__ out,
-                                                   int64_t ldo, const float* __restrict__ kv, int64_t layer_slots,
-                                                   int block_size, int hkv, int hd, float scale,
-                                                   const pia_attn_entry* __restrict__ entries,
-                                                   const int32_t* __restrict__ tables, int split, int nsplit,
-                                                   float* __restrict__ part_o, float* __restrict__ part_ml) {
+struct AttnParams {
+  const float* q;  // query rows (raw qkv rows when fused)
+  int64_t ldq;
+  float* out;
+  int64_t ldo;
+  float* kv;
+  int64_t layer_slots;  // layer * num_blocks * block_size
+  int block_size, hkv, hd, heads;
+  float scale;
+  const pia_attn_entry* entries;
+  const int32_t* tables;
+  int split, nsplit;
+  float* part_o;
+  float* part_ml;
+  int* counters;  // [n][hkv], zero between launches
+  const float* rope_cos;
+  const float* rope_sin;
+};
+
+// HD: compile-time head_dim (0 = runtime p.hd, for unusual shapes); every loop over the head
+// dimension and over the tokens of a split issues its loads before their first use.
+template <int G, int HD, int TPT, bool FUSED>
+__global__ __launch_bounds__(kThreads) void k_attn(AttnParams p) {
   extern __shared__ float smem[];
-  float* qs = smem;                                              // [G][hd]
-  float* sc = qs + G * hd;                                       // [G][kThreads]
-  float* stat = sc + G * kThreads;                               // [G][2]
-  int* slot_of = reinterpret_cast<int*>(stat + 2 * G);           // [kThreads]
-  float* red = reinterpret_cast<float*>(slot_of + kThreads);     // [ngrp][G][hd]
+  const int hd = HD ? HD : p.hd;
+  float* qs = smem;                                         // [G][hd]
+  float* sc = qs + G * hd;                                  // [G][kThreads]
+  float* stat = sc + G * kThreads;                          // [G][2]
+  float* knew = stat + 2 * G;                               // [hd]  (fused: this entry's k)
+  float* vnew = knew + hd;                                  // [hd]
+  int* slot_of = reinterpret_cast<int*>(vnew + hd);         // [kThreads]
+  int* flag = slot_of + kThreads;                           // [1]
+  float* red = reinterpret_cast<float*>(flag + 1);          // [ngrp][G][hd]
 
   const int s = blockIdx.x, kvh = blockIdx.y, e = blockIdx.z;
   const int tid = threadIdx.x;
-  const pia_attn_entry en = entries[e];
-  const int heads = hkv * G;
-  const int t0 = en.start + s * split;
-  const int t1 = min(en.pos + 1, t0 + split);
+  const pia_attn_entry en = p.entries[e];
+  const int t0 = en.start + s * p.split;
+  const int t1 = min(en.pos + 1, t0 + p.split);
   const int count = max(0, t1 - t0);
+  const int half = hd / 2;
+  const float* qrow = p.q + static_cast<int64_t>(e) * p.ldq;
+  const bool own = FUSED && en.pos >= t0 && en.pos < t1;  // this split holds the entry's token
+  const int64_t kv_head_stride = 2 * static_cast<int64_t>(hd);
+  auto kv_at = [&](int slot) { return p.kv + ((p.layer_slots + slot) * p.hkv + kvh) * kv_head_stride; };
 
-  for (int i = tid; i < G * hd; i += kThreads) qs[i] = q[static_cast<int64_t>(e) * ldq + kvh * G * hd + i];
   {
     int slot = -1;
-    const int t = t0 + tid;
     if (tid < count) {
-      const int lb = t / block_size;
-      if (lb < en.table_len) slot = tables[en.table_off + lb] * block_size + (t % block_size);
+      const int t = t0 + tid;
+      const int lb = t / p.block_size;
+      if (lb < en.table_len) slot = p.tables[en.table_off + lb] * p.block_size + (t % p.block_size);
     }
     slot_of[tid] = slot;
   }
+  if (FUSED) {
+    const float* c = p.rope_cos + static_cast<int64_t>(en.pos) * half;
+    const float* sn = p.rope_sin + static_cast<int64_t>(en.pos) * half;
+    for (int i = tid; i < G * half; i += kThreads) {
+      const int g = i / half, j = i % half;
+      const float* qh = qrow + (kvh * G + g) * hd;
+      const float a = qh[j], b = qh[j + half];
+      qs[g * hd + j] = a * c[j] - b * sn[j];
+      qs[g * hd + j + half] = b * c[j] + a * sn[j];
+    }
+    if (own) {
+      int own_slot = -1;
+      const int lb = en.pos / p.block_size;
+      if (lb < en.table_len) own_slot = p.tables[en.table_off + lb] * p.block_size + en.pos % p.block_size;
+      const float* kr = qrow + (p.heads + kvh) * hd;
+      const float* vr = qrow + (p.heads + p.hkv + kvh) * hd;
+      float* dst = own_slot >= 0 ? kv_at(own_slot) : nullptr;
+      for (int j = tid; j < half; j += kThreads) {
+        const float a = kr[j], b = kr[j + half];
+        const float r0 = a * c[j] - b * sn[j];
+        const float r1 = b * c[j] + a * sn[j];
+        knew[j] = r0;
+        knew[j + half] = r1;
+        if (dst) dst[j] = r0, dst[j + half] = r1;
+      }
+      for (int d = tid; d < hd; d += kThreads) {
+        vnew[d] = vr[d];
+        if (dst) dst[hd + d] = vr[d];
+      }
+    }
+  } else {
+    for (int i = tid; i < G * hd; i += kThreads) qs[i] = qrow[kvh * G * hd + i];
+  }
   __syncthreads();
 
-  // Scores: thread tid <-> token t0 + tid.
+  // Scores: TPT threads per token, each covering hd / TPT dims, reduced by lane shuffles.
   {
-    const int slot = slot_of[tid];
+    const int tok = tid / TPT, part = tid % TPT;
+    const int seg = hd / TPT;
+    const int slot = tok < count ? slot_of[tok] : -1;
     float acc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g] = 0.0f;
     if (slot >= 0) {
-      const float* kp = kv + ((static_cast<int64_t>(layer_slots) + slot) * hkv + kvh) * 2 * hd;
-      for (int d = 0; d < hd; d += 4) {
-        const float4 k4 = *reinterpret_cast<const float4*>(kp + d);
+      const float* kp = (FUSED && own && t0 + tok == en.pos) ? knew : kv_at(slot);
+      kp += part * seg;
+      const float* qp = qs + part * seg;
+      if constexpr (HD != 0) {
+        constexpr int kSeg = HD / TPT;
+        float4 k4[kSeg / 4];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float* qg = qs + g * hd + d;
-          acc[g] = __builtin_fmaf(qg[0], k4.x, acc[g]);
-          acc[g] = __builtin_fmaf(qg[1], k4.y, acc[g]);
-          acc[g] = __builtin_fmaf(qg[2], k4.z, acc[g]);
-          acc[g] = __builtin_fmaf(qg[3], k4.w, acc[g]);
+        for (int i = 0; i < kSeg / 4; ++i) k4[i] = reinterpret_cast<const float4*>(kp)[i];
+#pragma unroll
+        for (int i = 0; i < kSeg / 4; ++i)
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float4 q4 = reinterpret_cast<const float4*>(qp + g * HD)[i];
+            acc[g] = __builtin_fmaf(q4.x, k4[i].x, acc[g]);
+            acc[g] = __builtin_fmaf(q4.y, k4[i].y, acc[g]);
+            acc[g] = __builtin_fmaf(q4.z, k4[i].z, acc[g]);
+            acc[g] = __builtin_fmaf(q4.w, k4[i].w, acc[g]);
+          }
+      } else {
+        for (int d = 0; d < seg; d += 4) {
+          const float4 k4 = *reinterpret_cast<const float4*>(kp + d);
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float* qg = qp + g * hd + d;
+            acc[g] = __builtin_fmaf(qg[0], k4.x, acc[g]);
+            acc[g] = __builtin_fmaf(qg[1], k4.y, acc[g]);
+            acc[g] = __builtin_fmaf(qg[2], k4.z, acc[g]);
+            acc[g] = __builtin_fmaf(qg[3], k4.w, acc[g]);
+          }
         }
       }
-#pragma unroll
-      for (int g = 0; g < G; ++g) sc[g * kThreads + tid] = acc[g] * scale;
-    } else {
-#pragma unroll
-      for (int g = 0; g < G; ++g) sc[g * kThreads + tid] = -INFINITY;
     }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int off = TPT / 2; off >= 1; off >>= 1) acc[g] += __shfl_xor(acc[g], off, 64);
+    if (part == 0 && tok < p.split) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) sc[g * kThreads + tok] = slot >= 0 ? acc[g] * p.scale : -INFINITY;
+    }
+    for (int i = p.split + tid; i < kThreads; i += kThreads)
+#pragma unroll
+      for (int g = 0; g < G; ++g) sc[g * kThreads + i] = -INFINITY;
   }
   __syncthreads();
 
@@ -98,13 +186,15 @@ __global__ __launch_bounds__(kThreads) void k_attn(const float* __restrict__ q, 
     for (int g = wave; g < G; g += kThreads / 64) {
       float* row = sc + g * kThreads;
       float m = -INFINITY;
+#pragma unroll
       for (int i = lane; i < kThreads; i += 64) m = fmaxf(m, row[i]);
       m = wave_max(m);
       float l = 0.0f;
+#pragma unroll
       for (int i = lane; i < kThreads; i += 64) {
-        const float p = (m == -INFINITY) ? 0.0f : expf(row[i] - m);
-        row[i] = p;
-        l += p;
+        const float pr = (m == -INFINITY) ? 0.0f : expf(row[i] - m);
+        row[i] = pr;
+        l += pr;
       }
       l = wave_sum(l);
       if (lane == 0) {
@@ -115,32 +205,49 @@ __global__ __launch_bounds__(kThreads) void k_attn(const float* __restrict__ q, 
   }
   __syncthreads();
 
-  // V accumulation: hd/4 threads per token group, each owning 4 consecutive dims.
+  // V accumulation: hd/4 threads per token group, each owning 4 consecutive dims; 4 tokens'
+  // loads in flight per thread.
   const int tpg = hd / 4;
   const int ngrp = kThreads / tpg;
-  const int grp = tid / tpg, d4 = (tid % tpg) * 4;
-  if (grp < ngrp) {
-    float o[G][4];
+  {
+    const int grp = tid / tpg, d4 = (tid % tpg) * 4;
+    if (grp < ngrp) {
+      float o[G][4];
 #pragma unroll
-    for (int g = 0; g < G; ++g) o[g][0] = o[g][1] = o[g][2] = o[g][3] = 0.0f;
-    for (int i = grp; i < count; i += ngrp) {
-      const int slot = slot_of[i];
-      if (slot < 0) continue;
-      const float4 v4 =
-          *reinterpret_cast<const float4*>(kv + ((static_cast<int64_t>(layer_slots) + slot) * hkv + kvh) * 2 * hd + hd + d4);
+      for (int g = 0; g < G; ++g) o[g][0] = o[g][1] = o[g][2] = o[g][3] = 0.0f;
+      for (int i0 = grp; i0 < count; i0 += 4 * ngrp) {
+        float4 v4[4];
+        int idx[4];
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float p = sc[g * kThreads + i];
-        o[g][0] = __builtin_fmaf(p, v4.x, o[g][0]);
-        o[g][1] = __builtin_fmaf(p, v4.y, o[g][1]);
-        o[g][2] = __builtin_fmaf(p, v4.z, o[g][2]);
-        o[g][3] = __builtin_fmaf(p, v4.w, o[g][3]);
+        for (int u = 0; u < 4; ++u) {
+          const int i = i0 + u * ngrp;
+          const int slot = i < count ? slot_of[i] : -1;
+          idx[u] = slot >= 0 ? i : -1;
+          if (slot >= 0) {
+            const float* vp = (FUSED && own && t0 + i == en.pos) ? vnew : kv_at(slot) + hd;
+            v4[u] = *reinterpret_cast<const float4*>(vp + d4);
+          } else {
+            v4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (idx[u] < 0) continue;
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float pr = sc[g * kThreads + idx[u]];
+            o[g][0] = __builtin_fmaf(pr, v4[u].x, o[g][0]);
+            o[g][1] = __builtin_fmaf(pr, v4[u].y, o[g][1]);
+            o[g][2] = __builtin_fmaf(pr, v4[u].z, o[g][2]);
+            o[g][3] = __builtin_fmaf(pr, v4[u].w, o[g][3]);
+          }
+        }
       }
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) red[(grp * G + g) * hd + d4 + j] = o[g][j];
     }
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) red[(grp * G + g) * hd + d4 + j] = o[g][j];
   }
   __syncthreads();
 
@@ -149,110 +256,191 @@ __global__ __launch_bounds__(kThreads) void k_attn(const float* __restrict__ q, 
     for (int gr = 0; gr < ngrp; ++gr) acc += red[gr * G * hd + idx];
     const int g = idx / hd, d = idx % hd;
     const int h = kvh * G + g;
-    if (nsplit == 1) {
+    if (p.nsplit == 1) {
       const float l = stat[2 * g + 1];
-      out[static_cast<int64_t>(e) * ldo + h * hd + d] = l > 0.0f ? acc / l : 0.0f;
+      p.out[static_cast<int64_t>(e) * p.ldo + h * hd + d] = l > 0.0f ? acc / l : 0.0f;
     } else {
-      const int64_t ps = (static_cast<int64_t>(e) * heads + h) * nsplit + s;
-      part_o[ps * hd + d] = acc;
+      const int64_t ps = (static_cast<int64_t>(e) * p.heads + h) * p.nsplit + s;
+      p.part_o[ps * hd + d] = acc;
       if (d == 0) {
-        part_ml[2 * ps] = stat[2 * g];
-        part_ml[2 * ps + 1] = stat[2 * g + 1];
+        p.part_ml[2 * ps] = stat[2 * g];
+        p.part_ml[2 * ps + 1] = stat[2 * g + 1];
       }
     }
   }
-}
+  if (p.nsplit == 1) return;
 
-// Log-sum-exp combine of the token splits of one (entry, head).
-__global__ __launch_bounds__(kMaxHd) void k_attn_combine(const float* __restrict__ part_o,
-                                                         const float* __restrict__ part_ml, float* __restrict__ out,
-                                                         int64_t ldo, int heads, int hd, int nsplit) {
-  const int eh = blockIdx.x;
-  const int e = eh / heads, h = eh % heads;
-  const int d = threadIdx.x;
-  const float* ml = part_ml + static_cast<int64_t>(eh) * nsplit * 2;
-  float m = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) m = fmaxf(m, ml[2 * s]);
-  if (d >= hd) return;
-  float val = 0.0f;
-  if (m != -INFINITY) {
-    float l = 0.0f, acc = 0.0f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float ms = ml[2 * s];
-      if (ms == -INFINITY) continue;
-      const float w = expf(ms - m);
-      l = __builtin_fmaf(ml[2 * s + 1], w, l);
-      acc = __builtin_fmaf(part_o[(static_cast<int64_t>(eh) * nsplit + s) * hd + d], w, acc);
-    }
-    val = l > 0.0f ? acc / l : 0.0f;
+  // The last split of this (entry, kv head) to finish combines all of them.
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const int prev = atomicAdd(&p.counters[e * p.hkv + kvh], 1);
+    flag[0] = prev == p.nsplit - 1;
   }
-  out[static_cast<int64_t>(e) * ldo + h * hd + d] = val;
+  __syncthreads();
+  if (!flag[0]) return;
+  __threadfence();
+  const int ns = p.nsplit;
+  const int64_t head0 = static_cast<int64_t>(e) * p.heads + kvh * G;
+  // Split weights exp(m_k - M) / L per head, staged in LDS (sc holds G * kThreads floats).
+  float* wk = sc;  // [G][ns], ns <= kThreads / 2 (launch_attention guarantees it)
+  for (int i = tid; i < G * ns; i += kThreads) {
+    const int g = i / ns, k = i % ns;
+    wk[i] = __builtin_nontemporal_load(&p.part_ml[2 * ((head0 + g) * ns + k)]);
+    wk[G * ns + i] = __builtin_nontemporal_load(&p.part_ml[2 * ((head0 + g) * ns + k) + 1]);
+  }
+  __syncthreads();
+  {
+    const int wave = tid >> 6, lane = tid & 63;
+    for (int g = wave; g < G; g += kThreads / 64) {
+      float m = -INFINITY;
+      for (int k = lane; k < ns; k += 64) m = fmaxf(m, wk[g * ns + k]);
+      m = wave_max(m);
+      float l = 0.0f;
+      for (int k = lane; k < ns; k += 64) {
+        const float mk = wk[g * ns + k];
+        if (mk != -INFINITY) l = __builtin_fmaf(wk[G * ns + g * ns + k], expf(mk - m), l);
+      }
+      l = wave_sum(l);
+      for (int k = lane; k < ns; k += 64) {
+        const float mk = wk[g * ns + k];
+        wk[g * ns + k] = (m == -INFINITY || mk == -INFINITY || !(l > 0.0f)) ? 0.0f : expf(mk - m) / l;
+      }
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < G * hd; idx += kThreads) {
+    const int g = idx / hd, d = idx % hd;
+    const float* po = p.part_o + (head0 + g) * ns * hd + d;
+    const float* wg = wk + g * ns;
+    float acc = 0.0f;
+    int k = 0;
+    for (; k + 8 <= ns; k += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(po + static_cast<int64_t>(k + u) * hd);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(v[u], wg[k + u], acc);
+    }
+    for (; k < ns; ++k) acc = __builtin_fmaf(__builtin_nontemporal_load(po + static_cast<int64_t>(k) * hd), wg[k], acc);
+    p.out[static_cast<int64_t>(e) * p.ldo + (kvh * G + g) * hd + d] = acc;
+  }
+  if (tid == 0) atomicExch(&p.counters[e * p.hkv + kvh], 0);
 }
 
 size_t attn_smem_bytes(int g, int hd) {
   const int ngrp = kThreads / (hd / 4);
-  return sizeof(float) * (g * hd + g * kThreads + 2 * g) + sizeof(int) * kThreads + sizeof(float) * ngrp * g * hd;
+  return sizeof(float) * (g * hd + g * kThreads + 2 * g + 2 * hd) + sizeof(int) * (kThreads + 1) +
+         sizeof(float) * ngrp * g * hd;
+}
+
+template <int G, int HD, int TPT, bool F>
+void set_smem(size_t smem) {
+  static bool done = false;
+  if (!done && smem > 65536) {
+    PIA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn<G, HD, TPT, F>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
+    done = true;
+  }
+}
+
+template <int G, int HD, int TPT>
+void go(const AttnParams& p, dim3 grid, size_t smem, bool fused, hipStream_t st) {
+  if (fused) {
+    set_smem<G, HD, TPT, true>(smem);
+    hipLaunchKernelGGL((k_attn<G, HD, TPT, true>), grid, dim3(kThreads), smem, st, p);
+  } else {
+    set_smem<G, HD, TPT, false>(smem);
+    hipLaunchKernelGGL((k_attn<G, HD, TPT, false>), grid, dim3(kThreads), smem, st, p);
+  }
+}
+
+template <int G, int HD>
+void by_tpt(const AttnParams& p, dim3 grid, size_t smem, bool fused, hipStream_t st) {
+  const int tpt = kThreads / p.split;
+  if (tpt == 1) go<G, HD, 1>(p, grid, smem, fused, st);
+  else if (tpt == 2) go<G, HD, 2>(p, grid, smem, fused, st);
+  else go<G, HD, 4>(p, grid, smem, fused, st);
+}
+
+template <int G>
+void by_hd(const AttnParams& p, dim3 grid, size_t smem, bool fused, hipStream_t st) {
+  if (p.hd == 64) by_tpt<G, 64>(p, grid, smem, fused, st);
+  else if (p.hd == 128) by_tpt<G, 128>(p, grid, smem, fused, st);
+  else if (p.hd == 32) by_tpt<G, 32>(p, grid, smem, fused, st);
+  else by_tpt<G, 0>(p, grid, smem, fused, st);
 }
 
 }  // namespace
 
-int64_t attention_splits(int64_t max_window) { return max_window <= kThreads ? 1 : (max_window + kThreads - 1) / kThreads; }
+AttnPlan plan_attention(int64_t n, int64_t num_kv_heads, int64_t head_dim, int64_t max_window, int num_cus) {
+  // Widest split (fewest partials) that still gives ~2 workgroups per CU; a split of 64 or
+  // 128 tokens spreads each token over 4 or 2 threads, which needs head_dim % (4 * TPT) == 0.
+  AttnPlan plan{kThreads, 1};
+  const int64_t w = std::max<int64_t>(1, max_window);
+  for (int split : {256, 128, 64}) {
+    const int tpt = kThreads / split;
+    if (head_dim % (4 * tpt) != 0) break;
+    plan.split = split;
+    plan.splits = (w + split - 1) / split;
+    if (n * num_kv_heads * plan.splits >= 2 * static_cast<int64_t>(num_cus)) break;
+  }
+  return plan;
+}
 
 int64_t attention_work_bytes(int64_t n, int64_t heads, int64_t head_dim, int64_t splits) {
   if (splits <= 1) return 0;
   return n * heads * splits * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
 }
 
-void launch_attention(const float* q, int64_t ldq, float* out, int64_t ldo, const float* kv,
-                      const pia_kv_layout& L, int64_t heads, const pia_attn_entry* entries, const int32_t* tables,
-                      int64_t n, int64_t layer, int64_t splits, void* work, hipStream_t st) {
-  PIA_REQUIRE(L.num_kv_heads > 0 && heads % L.num_kv_heads == 0,
+void launch_attention(const AttnLaunch& a, hipStream_t st) {
+  const pia_kv_layout& L = *a.layout;
+  PIA_REQUIRE(L.num_kv_heads > 0 && a.heads % L.num_kv_heads == 0,
               "attention: num_heads must be a multiple of num_kv_heads");
   PIA_REQUIRE(L.head_dim % 4 == 0 && L.head_dim <= kMaxHd, "attention: head_dim must be a multiple of 4 and <= 128");
-  PIA_REQUIRE(layer >= 0 && layer < L.num_layers, "attention: layer out of range");
+  PIA_REQUIRE(a.layer >= 0 && a.layer < L.num_layers, "attention: layer out of range");
   PIA_REQUIRE(L.num_blocks * L.block_size < (int64_t(1) << 31), "attention: too many cache slots for int32 indexing");
-  PIA_REQUIRE(splits >= 1 && splits < 65536, "attention: bad split count");
-  PIA_REQUIRE(splits == 1 || work != nullptr, "attention: split-K needs a workspace");
-  if (n == 0) return;
-  const int g = static_cast<int>(heads / L.num_kv_heads);
+  PIA_REQUIRE(a.plan.splits >= 1 && a.plan.splits <= kThreads / 2,
+              "attention: at most 128 token splits (windows up to 32768 tokens)");
+  PIA_REQUIRE(a.plan.split == 64 || a.plan.split == 128 || a.plan.split == 256, "attention: bad split size");
+  PIA_REQUIRE(L.head_dim % (4 * (kThreads / a.plan.split)) == 0, "attention: split size does not fit head_dim");
+  PIA_REQUIRE(a.plan.splits == 1 || (a.work && a.counters), "attention: split-K needs a workspace and counters");
+  PIA_REQUIRE(!a.fused || (a.rope_cos && a.rope_sin), "attention: fused RoPE needs the rotary tables");
+  if (a.n == 0) return;
+  const int g = static_cast<int>(a.heads / L.num_kv_heads);
   const int hd = static_cast<int>(L.head_dim);
-  const float scale = 1.0f / sqrtf(static_cast<float>(hd));
-  const int64_t layer_slots = layer * L.num_blocks * L.block_size;
-  float* part_o = static_cast<float*>(work);
-  float* part_ml = part_o ? part_o + n * heads * splits * hd : nullptr;
-  dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(L.num_kv_heads), static_cast<unsigned>(n));
+  AttnParams p;
+  p.q = a.q;
+  p.ldq = a.ldq;
+  p.out = a.out;
+  p.ldo = a.ldo;
+  p.kv = a.kv;
+  p.layer_slots = a.layer * L.num_blocks * L.block_size;
+  p.block_size = static_cast<int>(L.block_size);
+  p.hkv = static_cast<int>(L.num_kv_heads);
+  p.hd = hd;
+  p.heads = static_cast<int>(a.heads);
+  p.scale = 1.0f / sqrtf(static_cast<float>(hd));
+  p.entries = a.entries;
+  p.tables = a.tables;
+  p.split = static_cast<int>(a.plan.split);
+  p.nsplit = static_cast<int>(a.plan.splits);
+  p.part_o = static_cast<float*>(a.work);
+  p.part_ml = p.part_o ? p.part_o + a.n * a.heads * a.plan.splits * hd : nullptr;
+  p.counters = a.counters;
+  p.rope_cos = a.rope_cos;
+  p.rope_sin = a.rope_sin;
+  dim3 grid(static_cast<unsigned>(a.plan.splits), static_cast<unsigned>(L.num_kv_heads), static_cast<unsigned>(a.n));
   const size_t smem = attn_smem_bytes(g, hd);
-  const int bs = static_cast<int>(L.block_size), hkv = static_cast<int>(L.num_kv_heads);
-  const int ns = static_cast<int>(splits);
-#define PIA_ATTN_CASE(GV)                                                                                  \
-  case GV:                                                                                                 \
-    hipLaunchKernelGGL(k_attn<GV>, grid, dim3(kThreads), smem, st, q, ldq, out, ldo, kv, layer_slots, bs, hkv, \
-                       hd, scale, entries, tables, kThreads, ns, part_o, part_ml);                         \
-    break;
-  if (smem > 65536) {
-    static bool raised[17] = {};
-    if (!raised[g]) {
-      const void* fn = g == 16 ? reinterpret_cast<const void*>(k_attn<16>) : reinterpret_cast<const void*>(k_attn<8>);
-      PIA_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
-      raised[g] = true;
-    }
-  }
   switch (g) {
-    PIA_ATTN_CASE(1)
-    PIA_ATTN_CASE(2)
-    PIA_ATTN_CASE(4)
-    PIA_ATTN_CASE(8)
-    PIA_ATTN_CASE(16)
-    default:
-      fail(PIA_ERR_INVALID, "attention: kv_group must be 1, 2, 4, 8 or 16");
+    case 1: by_hd<1>(p, grid, smem, a.fused, st); break;
+    case 2: by_hd<2>(p, grid, smem, a.fused, st); break;
+    case 4: by_hd<4>(p, grid, smem, a.fused, st); break;
+    case 8: by_hd<8>(p, grid, smem, a.fused, st); break;
+    case 16: by_hd<16>(p, grid, smem, a.fused, st); break;
+    default: fail(PIA_ERR_INVALID, "attention: kv_group must be 1, 2, 4, 8 or 16");
   }
-#undef PIA_ATTN_CASE
   PIA_HIP(hipGetLastError());
-  if (splits > 1) {
-    hipLaunchKernelGGL(k_attn_combine, dim3(static_cast<unsigned>(n * heads)), dim3(kMaxHd), 0, st, part_o, part_ml,
-                       out, ldo, static_cast<int>(heads), hd, ns);
-    PIA_HIP(hipGetLastError());
-  }
 }
 
 }  // namespace pia

@@ -28,8 +28,10 @@ __device__ inline float block_sum(float v, float* red) {
 }
 
 __global__ __launch_bounds__(kThreads) void k_embed(const int32_t* __restrict__ tokens, const uint16_t* __restrict__ emb,
-                                                    float* __restrict__ x, int64_t ldx, int64_t hidden, int64_t vocab) {
+                                                    float* __restrict__ x, int64_t ldx, int64_t hidden, int64_t vocab,
+                                                    unsigned long long* __restrict__ amax) {
   const int b = blockIdx.x;
+  if (amax && threadIdx.x == 0) amax[b] = 0ull;
   const int64_t tok = static_cast<int64_t>(static_cast<uint32_t>(tokens[b])) % vocab;
   const uint16_t* src = emb + tok * hidden;
   float* dst = x + static_cast<int64_t>(b) * ldx;
@@ -187,10 +189,10 @@ __global__ __launch_bounds__(kThreads) void k_copy_block(float* __restrict__ kv,
 }  // namespace
 
 void launch_embed(const int32_t* tokens, const uint16_t* embed, float* x, int64_t ldx, int64_t batch, int64_t hidden,
-                  int64_t vocab, hipStream_t st) {
+                  int64_t vocab, unsigned long long* amax, hipStream_t st) {
   if (batch == 0) return;
   hipLaunchKernelGGL(k_embed, dim3(static_cast<unsigned>(batch)), dim3(kThreads), 0, st, tokens, embed, x, ldx, hidden,
-                     vocab);
+                     vocab, amax);
   PIA_HIP(hipGetLastError());
 }
 
@@ -246,4 +248,27 @@ void launch_copy_block(float* kv, const pia_kv_layout& L, int64_t src, int64_t d
   PIA_HIP(hipGetLastError());
 }
 
+}  // namespace pia
+
+namespace pia {
+namespace {
+__global__ void k_spin(uint64_t ticks) {
+  const uint64_t t0 = wall_clock64();
+  while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(32);
+}
+}  // namespace
+
+void launch_spin(double us, hipStream_t st) {
+  PIA_REQUIRE(us >= 0 && us <= 20000, "spin: at most 20 ms");
+  static int rate_khz = 0;
+  if (!rate_khz) {
+    int dev = 0;
+    PIA_HIP(hipGetDevice(&dev));
+    PIA_HIP(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, dev));
+    if (rate_khz <= 0) rate_khz = 100000;
+  }
+  const uint64_t ticks = static_cast<uint64_t>(us * rate_khz / 1000.0);
+  hipLaunchKernelGGL(k_spin, dim3(1), dim3(1), 0, st, ticks);
+  PIA_HIP(hipGetLastError());
+}
 }  // namespace pia

@@ -1,55 +1,69 @@
-// Weight-streaming projection for decode batches (batch 1..15): one wavefront owns R output
-// rows; each lane streams VEC contiguous weight elements per step (16 int8 = one 128-bit
-// load), widens them in registers and accumulates in f32 against the activation vectors of
-// up to NB batch entries, so every weight byte is fetched from HBM once per launch. The
-// per-row scale is applied after the wavefront reduction, as the reference does
-// (src/math.rs:486-492: dot_i8(row, x) * scale).
+// Weight-streaming projection for small decode batches: one wavefront owns R output rows;
+// each lane streams VEC contiguous weight elements per step (16 int8 = one 128-bit load),
+// widens them in registers and accumulates in f32 against the activation vectors of the
+// batch, so every weight byte is fetched from HBM once per launch. The per-row scale is
+// applied after the wavefront reduction, as the reference does (src/math.rs:486-492:
+// dot_i8(row, x) * scale).
+//
+// Fusions (each removes a launch and a round trip of the activations through HBM):
+//   - prologue RMSNorm (src/math.rs:4-22): when `norm_w` is given the workgroup computes
+//     1/rms of every batch row itself and normalizes x on the fly;
+//   - epilogue residual add (src/model.rs:1127-1129, 1165-1167): out += proj;
+//   - epilogue SwiGLU (src/math.rs:293-302): gate and up rows are interleaved in HBM
+//     (row 2i = gate i, row 2i+1 = up i) and the wave that owns both writes silu(g) * u.
 #include "common.h"
 #include "kernels.h"
 
 namespace pia {
 namespace {
 
+// Raw weight registers for VEC elements, loaded with one vector instruction, widened later.
 template <typename TW, int VEC>
-__device__ inline void load_w(const TW* p, float (&w)[VEC]);
-
+struct Raw;
 template <>
-__device__ inline void load_w<int8_t, 16>(const int8_t* p, float (&w)[16]) {
-  const int4 v = *reinterpret_cast<const int4*>(p);
-  const int d[4] = {v.x, v.y, v.z, v.w};
+struct Raw<int8_t, 16> {
+  int4 v;
+  __device__ void load(const int8_t* p) { v = *reinterpret_cast<const int4*>(p); }
+  __device__ void zero() { v = make_int4(0, 0, 0, 0); }
+  __device__ void widen(float (&w)[16]) const {
+    const int d[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-  for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < 4; ++k)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w[4 * k + j] = static_cast<float>((d[k] << (24 - 8 * j)) >> 24);
-}
+      for (int j = 0; j < 4; ++j) w[4 * k + j] = static_cast<float>((d[k] << (24 - 8 * j)) >> 24);
+  }
+};
 template <>
-__device__ inline void load_w<int8_t, 8>(const int8_t* p, float (&w)[8]) {
-  const int2 v = *reinterpret_cast<const int2*>(p);
-  const int d[2] = {v.x, v.y};
+struct Raw<int8_t, 4> {
+  int v;
+  __device__ void load(const int8_t* p) { v = *reinterpret_cast<const int*>(p); }
+  __device__ void zero() { v = 0; }
+  __device__ void widen(float (&w)[4]) const {
 #pragma unroll
-  for (int k = 0; k < 2; ++k)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[4 * k + j] = static_cast<float>((d[k] << (24 - 8 * j)) >> 24);
-}
+    for (int j = 0; j < 4; ++j) w[j] = static_cast<float>((v << (24 - 8 * j)) >> 24);
+  }
+};
 template <>
-__device__ inline void load_w<int8_t, 4>(const int8_t* p, float (&w)[4]) {
-  const int d = *reinterpret_cast<const int*>(p);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) w[j] = static_cast<float>((d << (24 - 8 * j)) >> 24);
-}
+struct Raw<int8_t, 1> {
+  int8_t v;
+  __device__ void load(const int8_t* p) { v = *p; }
+  __device__ void zero() { v = 0; }
+  __device__ void widen(float (&w)[1]) const { w[0] = static_cast<float>(v); }
+};
 template <>
-__device__ inline void load_w<int8_t, 1>(const int8_t* p, float (&w)[1]) {
-  w[0] = static_cast<float>(*p);
-}
+struct Raw<float, 4> {
+  float4 v;
+  __device__ void load(const float* p) { v = *reinterpret_cast<const float4*>(p); }
+  __device__ void zero() { v = make_float4(0.f, 0.f, 0.f, 0.f); }
+  __device__ void widen(float (&w)[4]) const { w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w; }
+};
 template <>
-__device__ inline void load_w<float, 4>(const float* p, float (&w)[4]) {
-  const float4 v = *reinterpret_cast<const float4*>(p);
-  w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
-}
-template <>
-__device__ inline void load_w<float, 1>(const float* p, float (&w)[1]) {
-  w[0] = *p;
-}
+struct Raw<float, 1> {
+  float v;
+  __device__ void load(const float* p) { v = *p; }
+  __device__ void zero() { v = 0.f; }
+  __device__ void widen(float (&w)[1]) const { w[0] = v; }
+};
 
 template <int VEC>
 __device__ inline void load_x(const float* p, float (&x)[VEC]) {
@@ -72,24 +86,78 @@ __device__ inline float wave_sum(float v) {
 }
 
 constexpr int kWaves = 4;  // wavefronts per workgroup
+constexpr int kMaxNormBatch = 64;
 
-template <typename TW, int VEC, int R, int NB, int EPI>
+enum { kEpiStore = 0, kEpiAdd = 1, kEpiSwiglu = 2 };
+
+// f32 -> u32 preserving f32::total_cmp order (src/sampling.rs:140-147 compares with total_cmp).
+__device__ inline uint32_t order_key(float f) {
+  const uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ inline unsigned long long wave_max_u64(unsigned long long v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const unsigned long long o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// UNR chunks of 64*VEC columns per load batch: every weight load of a batch is issued before
+// the first use, so a wavefront pays one HBM round trip per batch, not one per chunk.
+template <typename TW, int VEC, int R, int NB, int UNR, int EPI, bool NORM, bool AMAX>
 __global__ __launch_bounds__(64 * kWaves) void k_gemv(const TW* __restrict__ W, int64_t ldw,
                                                       const float* __restrict__ S, const float* __restrict__ X,
-                                                      int64_t ldx, float* __restrict__ O, int64_t osb, int64_t osr,
-                                                      int rows, int cols, int batch) {
-  const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * R;
-  if (row0 >= rows) return;
-
+                                                      int64_t ldx, const float* __restrict__ NW, float eps,
+                                                      float* __restrict__ O, int64_t osb, int64_t osr, int rows,
+                                                      int cols, int batch, unsigned long long* __restrict__ amax) {
+  __shared__ float inv_s[NORM ? kMaxNormBatch : 1];
+  __shared__ float red[kWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * kWaves + wave) * R;
   const TW* wrow[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) wrow[r] = W + static_cast<int64_t>(min(row0 + r, rows - 1)) * ldw;
   const int main_cols = cols - cols % VEC;
   const int rem = cols - main_cols;
+  constexpr int kStep = 64 * VEC * UNR;
 
-  // Batch groups run back to back over the same R weight rows: the first group streams them
-  // from HBM, later groups hit in cache.
+  Raw<TW, VEC> raw[UNR][R];
+  auto load_batch = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int c = base + (u * 64 + lane) * VEC;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (c < main_cols) raw[u][r].load(wrow[r] + c);
+        else raw[u][r].zero();
+      }
+    }
+  };
+  load_batch(0);  // in flight while the RMSNorm prologue runs
+
+  if constexpr (NORM) {
+    // 1/rms of each batch row (src/math.rs:12-18), computed by the whole workgroup.
+    for (int b = 0; b < batch; ++b) {
+      const float* xr = X + static_cast<int64_t>(b) * ldx;
+      float ss = 0.0f;
+      for (int i = threadIdx.x; i < cols; i += 64 * kWaves) ss += xr[i] * xr[i];
+      ss = wave_sum(ss);
+      if (lane == 0) red[wave] = ss;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) t += red[w];
+        inv_s[b] = 1.0f / sqrtf(t / static_cast<float>(cols) + eps);
+      }
+      __syncthreads();
+    }
+  }
+  if (row0 >= rows) return;
+
   for (int b0 = 0; b0 < batch; b0 += NB) {
     float acc[R][NB];
 #pragma unroll
@@ -97,30 +165,46 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv(const TW* __restrict__ W, 
 #pragma unroll
       for (int b = 0; b < NB; ++b) acc[r][b] = 0.0f;
 
-    for (int c = lane * VEC; c < main_cols; c += 64 * VEC) {
-      float w[R][VEC];
+    for (int base = 0; base < main_cols; base += kStep) {
+      if (base != 0 || b0 != 0) load_batch(base);
 #pragma unroll
-      for (int r = 0; r < R; ++r) load_w<TW, VEC>(wrow[r] + c, w[r]);
+      for (int u = 0; u < UNR; ++u) {
+        const int c = base + (u * 64 + lane) * VEC;
+        if (c < main_cols) {
+          float nw[VEC];
+          if constexpr (NORM) load_x<VEC>(NW + c, nw);
+          float w[R][VEC];
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        if (b0 + b < batch) {
-          float xv[VEC];
-          load_x<VEC>(X + static_cast<int64_t>(b0 + b) * ldx + c, xv);
+          for (int r = 0; r < R; ++r) raw[u][r].widen(w[r]);
 #pragma unroll
-          for (int r = 0; r < R; ++r)
+          for (int b = 0; b < NB; ++b) {
+            if (b0 + b < batch) {
+              float xv[VEC];
+              load_x<VEC>(X + static_cast<int64_t>(b0 + b) * ldx + c, xv);
+              if constexpr (NORM) {
+                const float inv = inv_s[b0 + b];
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) acc[r][b] = __builtin_fmaf(w[r][j], xv[j], acc[r][b]);
+                for (int j = 0; j < VEC; ++j) xv[j] = (xv[j] * inv) * nw[j];
+              }
+#pragma unroll
+              for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) acc[r][b] = __builtin_fmaf(w[r][j], xv[j], acc[r][b]);
+            }
+          }
         }
       }
     }
     if (lane < rem) {
       const int c = main_cols + lane;
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float w = static_cast<float>(wrow[r][c]);
+      for (int b = 0; b < NB; ++b) {
+        if (b0 + b < batch) {
+          float xv = X[static_cast<int64_t>(b0 + b) * ldx + c];
+          if constexpr (NORM) xv = (xv * inv_s[b0 + b]) * NW[c];
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
-          if (b0 + b < batch) acc[r][b] = __builtin_fmaf(w, X[static_cast<int64_t>(b0 + b) * ldx + c], acc[r][b]);
+          for (int r = 0; r < R; ++r) acc[r][b] = __builtin_fmaf(static_cast<float>(wrow[r][c]), xv, acc[r][b]);
+        }
       }
     }
 
@@ -132,76 +216,137 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv(const TW* __restrict__ W, 
         const float s = wave_sum(acc[r][b]);
         if (lane == r * NB + b) mine = s;
       }
-    if (lane < R * NB) {
-      const int r = lane / NB, b = lane % NB;
-      const int row = row0 + r, bb = b0 + b;
-      if (row < rows && bb < batch) {
-        const float v = S ? mine * S[row] : mine;
+    const int r_l = lane / NB, b_l = lane % NB;
+    const int row = row0 + r_l, bb = b0 + b_l;
+    if constexpr (EPI == kEpiSwiglu) {
+      // Lanes (r, b) and (r + 1, b) hold the gate and up results of output row (row0 + r) / 2.
+      const float up = __shfl_down(mine, NB, 64);
+      if (lane < R * NB && (r_l & 1) == 0 && row + 1 < rows && bb < batch) {
+        const float g = S ? mine * S[row] : mine;
+        const float u = S ? up * S[row + 1] : up;
+        const float silu = g / (1.0f + expf(-g));
+        O[static_cast<int64_t>(bb) * osb + static_cast<int64_t>(row >> 1) * osr] = silu * u;
+      }
+    } else {
+      const bool valid = lane < R * NB && row < rows && bb < batch;
+      float v = 0.0f;
+      if (valid) {
+        v = S ? mine * S[row] : mine;
         float* o = O + static_cast<int64_t>(bb) * osb + static_cast<int64_t>(row) * osr;
-        if (EPI == 1) *o = *o + v;
+        if (EPI == kEpiAdd) *o = *o + v;
         else *o = v;
+      }
+      if constexpr (AMAX) {
+        // Greedy argmax fused into the LM head: max of (order key, row) per batch row; ties in
+        // the key keep the larger row, i.e. the last maximal index.
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          unsigned long long cand = 0;
+          if (valid && b_l == b)
+            cand = (static_cast<unsigned long long>(order_key(v)) << 32) | static_cast<uint32_t>(row);
+          cand = wave_max_u64(cand);
+          // Most waves lose to the running maximum: test before taking the atomic, so only a
+          // few of the thousands of waves contend on the slot.
+          if (lane == 0 && b0 + b < batch &&
+              cand > __hip_atomic_load(&amax[b0 + b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+            atomicMax(&amax[b0 + b], cand);
+        }
       }
     }
   }
 }
 
+struct Launch {
+  const void* W;
+  int64_t ldw;
+  const float* S;
+  const float* X;
+  int64_t ldx;
+  const float* NW;
+  float eps;
+  float* O;
+  int64_t osb, osr;
+  int rows, cols, batch;
+  unsigned long long* amax;
+  hipStream_t st;
+};
+
+template <typename TW, int VEC, int R, int NB, int UNR, int EPI>
+void go(const Launch& a) {
+  dim3 grid((a.rows + kWaves * R - 1) / (kWaves * R));
+  const TW* w = static_cast<const TW*>(a.W);
+#define PIA_GEMV_LAUNCH(NORM, AMAX)                                                                       \
+  hipLaunchKernelGGL((k_gemv<TW, VEC, R, NB, UNR, EPI, NORM, AMAX>), grid, dim3(64 * kWaves), 0, a.st, w, \
+                     a.ldw, a.S, a.X, a.ldx, a.NW, a.eps, a.O, a.osb, a.osr, a.rows, a.cols, a.batch, a.amax)
+  if constexpr (EPI == kEpiStore) {
+    if (a.amax) {
+      if (a.NW) PIA_GEMV_LAUNCH(true, true);
+      else PIA_GEMV_LAUNCH(false, true);
+      return;
+    }
+  }
+  if (a.NW) PIA_GEMV_LAUNCH(true, false);
+  else PIA_GEMV_LAUNCH(false, false);
+#undef PIA_GEMV_LAUNCH
+}
+
+template <typename TW, int VEC, int R, int NB, int UNR>
+void by_epi(const Launch& a, Epi epi) {
+  if (epi == Epi::Add) go<TW, VEC, R, NB, UNR, kEpiAdd>(a);
+  else if (epi == Epi::Swiglu) go<TW, VEC, R, NB, UNR, kEpiSwiglu>(a);
+  else go<TW, VEC, R, NB, UNR, kEpiStore>(a);
+}
+
 template <typename TW, int VEC, int R, int NB>
-void dispatch_epi(const TW* W, int64_t ldw, const float* S, const float* X, int64_t ldx, float* O, int64_t osb,
-                  int64_t osr, int rows, int cols, int batch, Epi epi, hipStream_t st) {
-  dim3 grid((rows + kWaves * R - 1) / (kWaves * R));
-  if (epi == Epi::Add)
-    hipLaunchKernelGGL((k_gemv<TW, VEC, R, NB, 1>), grid, dim3(64 * kWaves), 0, st, W, ldw, S, X, ldx, O, osb, osr,
-                       rows, cols, batch);
-  else
-    hipLaunchKernelGGL((k_gemv<TW, VEC, R, NB, 0>), grid, dim3(64 * kWaves), 0, st, W, ldw, S, X, ldx, O, osb, osr,
-                       rows, cols, batch);
+void by_unr(const Launch& a, Epi epi) {
+  // Chunks of 64*VEC columns a lane covers; batches of up to 8 chunks in flight per lane.
+  const int chunks = (a.cols / VEC + 63) / 64;
+  if (chunks <= 1) by_epi<TW, VEC, R, NB, 1>(a, epi);
+  else if (chunks <= 2) by_epi<TW, VEC, R, NB, 2>(a, epi);
+  else if (chunks <= 4) by_epi<TW, VEC, R, NB, 4>(a, epi);
+  else if (chunks <= 6) by_epi<TW, VEC, R, NB, 6>(a, epi);
+  else by_epi<TW, VEC, R, NB, 8>(a, epi);
 }
 
 template <typename TW, int VEC, int R>
-void dispatch_nb(const TW* W, int64_t ldw, const float* S, const float* X, int64_t ldx, float* O, int64_t osb,
-                 int64_t osr, int rows, int cols, int batch, Epi epi, hipStream_t st) {
-  if (batch == 1) dispatch_epi<TW, VEC, R, 1>(W, ldw, S, X, ldx, O, osb, osr, rows, cols, batch, epi, st);
-  else if (batch == 2) dispatch_epi<TW, VEC, R, 2>(W, ldw, S, X, ldx, O, osb, osr, rows, cols, batch, epi, st);
-  else if (batch <= 4) dispatch_epi<TW, VEC, R, 4>(W, ldw, S, X, ldx, O, osb, osr, rows, cols, batch, epi, st);
-  else dispatch_epi<TW, VEC, R, 8>(W, ldw, S, X, ldx, O, osb, osr, rows, cols, batch, epi, st);
+void by_nb(const Launch& a, Epi epi) {
+  if (a.batch == 1) by_unr<TW, VEC, R, 1>(a, epi);
+  else if (a.batch == 2) by_unr<TW, VEC, R, 2>(a, epi);
+  else by_unr<TW, VEC, R, 4>(a, epi);
 }
 
 template <typename TW, int VEC>
-void dispatch_r(const TW* W, int64_t ldw, const float* S, const float* X, int64_t ldx, float* O, int64_t osb,
-                int64_t osr, int rows, int cols, int batch, Epi epi, hipStream_t st) {
-  // Prefer 4 rows per wavefront (more bytes in flight per lane); fall back to fewer rows
-  // when that would leave most of the 256 CUs idle.
-  if (rows >= 4 * kWaves * 512) dispatch_nb<TW, VEC, 4>(W, ldw, S, X, ldx, O, osb, osr, rows, cols, batch, epi, st);
-  else if (rows >= 2 * kWaves * 256) dispatch_nb<TW, VEC, 2>(W, ldw, S, X, ldx, O, osb, osr, rows, cols, batch, epi, st);
-  else dispatch_nb<TW, VEC, 1>(W, ldw, S, X, ldx, O, osb, osr, rows, cols, batch, epi, st);
+void by_r(const Launch& a, Epi epi) {
+  // 4 rows per wavefront for tall matrices; 2 when that would leave CUs idle (2 is the
+  // smallest tile that keeps a SwiGLU gate/up pair in one wavefront).
+  if (a.rows >= 4 * kWaves * 512) by_nb<TW, VEC, 4>(a, epi);
+  else by_nb<TW, VEC, 2>(a, epi);
 }
 
 inline bool aligned(const void* p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 }  // namespace
 
-void launch_gemv(int wkind, const void* W, int64_t ldw, const float* scales, const float* x, int64_t ldx, float* out,
-                 int64_t osb, int64_t osr, int64_t rows, int64_t cols, int64_t batch, Epi epi, hipStream_t st) {
-  PIA_REQUIRE(rows > 0 && cols > 0 && batch > 0, "gemv: empty shape");
-  PIA_REQUIRE(rows < (int64_t(1) << 31) && cols < (int64_t(1) << 31) && batch < (int64_t(1) << 31),
+void launch_gemv(const GemvArgs& g, hipStream_t st) {
+  PIA_REQUIRE(g.rows > 0 && g.cols > 0 && g.batch > 0, "gemv: empty shape");
+  PIA_REQUIRE(g.rows < (int64_t(1) << 31) && g.cols < (int64_t(1) << 31) && g.batch < (int64_t(1) << 31),
               "gemv: shape exceeds int32 indexing");
-  PIA_REQUIRE(ldw >= cols && ldx >= cols, "gemv: leading dimension smaller than cols");
-  const int r = static_cast<int>(rows), c = static_cast<int>(cols), b = static_cast<int>(batch);
-  if (wkind == 1) {
-    PIA_REQUIRE(scales != nullptr, "gemv: int8 weights need scales");
-    const auto* w = static_cast<const int8_t*>(W);
-    if (ldw % 16 == 0 && ldx % 16 == 0 && aligned(w, 16) && aligned(x, 64))
-      dispatch_r<int8_t, 16>(w, ldw, scales, x, ldx, out, osb, osr, r, c, b, epi, st);
-    else if (ldw % 4 == 0 && ldx % 4 == 0 && aligned(w, 4) && aligned(x, 16))
-      dispatch_r<int8_t, 4>(w, ldw, scales, x, ldx, out, osb, osr, r, c, b, epi, st);
-    else
-      dispatch_r<int8_t, 1>(w, ldw, scales, x, ldx, out, osb, osr, r, c, b, epi, st);
+  PIA_REQUIRE(g.ldw >= g.cols && g.ldx >= g.cols, "gemv: leading dimension smaller than cols");
+  PIA_REQUIRE(!g.norm_w || g.batch <= kMaxNormBatch, "gemv: fused RMSNorm supports at most 64 rows");
+  PIA_REQUIRE(g.epi != Epi::Swiglu || g.rows % 2 == 0, "gemv: SwiGLU epilogue needs interleaved row pairs");
+  PIA_REQUIRE(!g.amax || g.epi == Epi::Store, "gemv: fused argmax needs the Store epilogue");
+  Launch a{g.W, g.ldw, g.scales, g.x, g.ldx, g.norm_w, g.eps, g.out, g.osb, g.osr,
+           static_cast<int>(g.rows), static_cast<int>(g.cols), static_cast<int>(g.batch), g.amax, st};
+  const bool xv16 = g.ldx % 16 == 0 && aligned(g.x, 64) && (!g.norm_w || aligned(g.norm_w, 64));
+  const bool xv4 = g.ldx % 4 == 0 && aligned(g.x, 16) && (!g.norm_w || aligned(g.norm_w, 16));
+  if (g.wkind == 1) {
+    PIA_REQUIRE(g.scales != nullptr, "gemv: int8 weights need scales");
+    if (g.ldw % 16 == 0 && aligned(g.W, 16) && xv16) by_r<int8_t, 16>(a, g.epi);
+    else if (g.ldw % 4 == 0 && aligned(g.W, 4) && xv4) by_r<int8_t, 4>(a, g.epi);
+    else by_r<int8_t, 1>(a, g.epi);
   } else {
-    const auto* w = static_cast<const float*>(W);
-    if (ldw % 4 == 0 && ldx % 4 == 0 && aligned(w, 16) && aligned(x, 16))
-      dispatch_r<float, 4>(w, ldw, scales, x, ldx, out, osb, osr, r, c, b, epi, st);
-    else
-      dispatch_r<float, 1>(w, ldw, scales, x, ldx, out, osb, osr, r, c, b, epi, st);
+    if (g.ldw % 4 == 0 && aligned(g.W, 16) && xv4) by_r<float, 4>(a, g.epi);
+    else by_r<float, 1>(a, g.epi);
   }
   PIA_HIP(hipGetLastError());
 }

@@ -114,6 +114,7 @@ _SIGS = {
     "pia_model_prefill": (I32, [P, P, I64, I64, P, I64, P, P]),
     "pia_model_profile": (I32, [P, I32]),
     "pia_model_profile_get": (I32, [P, P, P, I32]),
+    "pia_bench_projection": (I32, [P, I64, I64, I64, I32, C.POINTER(C.c_double), C.POINTER(I64)]),
     "pia_synth_normal": (I32, [U64, U64, F32, P, I64]),
     "pia_f32_to_bf16": (I32, [P, P, I64]),
 }
@@ -251,6 +252,13 @@ class DeviceArray:
             self.free()
         except Exception:
             pass
+
+
+def bench_projection(ctx: "Context", rows: int, cols: int, batch: int = 1, reps: int = 20):
+    """(microseconds per launch, algorithmic bytes per launch) of one int8 projection shape."""
+    us, by = C.c_double(), I64()
+    check(lib().pia_bench_projection(ctx.h, rows, cols, batch, reps, C.byref(us), C.byref(by)))
+    return us.value, by.value
 
 
 # ------------------------------------------------------------------------------------------

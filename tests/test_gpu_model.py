@@ -147,8 +147,18 @@ def test_config3_shape_batched_paged_decode(ctx):
         print(f"[config3] step {s} rel={rel:.3g}", flush=True)
         assert toks_g == toks_c
         assert rel <= LOGIT_TOL
-    # The decode writes landed in the same slots (values differ only by projection rounding).
-    assert np.allclose(gm.kv_download(), kv, rtol=1e-4, atol=1e-5)
+    # The decode writes landed in the same slots: every other slot is untouched (bit-exact) and
+    # the written K/V rows agree up to projection rounding.
+    got = gm.kv_download().reshape(cfg.layers, nb * bs, -1)
+    ref = kv.reshape(cfg.layers, nb * bs, -1)
+    written = np.zeros(nb * bs, bool)
+    for b in range(B):
+        for s in range(steps):
+            p = int(ctxs[b]) + s
+            written[tables[b][p // bs] * bs + p % bs] = True
+    assert np.array_equal(got[:, ~written], ref[:, ~written])
+    scale = np.max(np.abs(ref[:, written]))
+    assert np.max(np.abs(got[:, written] - ref[:, written])) <= 1e-4 * scale
     gm.close()
 
 
@@ -207,5 +217,6 @@ def test_prefix_sharing_and_cow_workload(ctx):
             s[4], s[5], s[3] = int(am[b]), orc.argmax(lc[b]), s[3] + 1
     assert mg.stats()["cow_copies"] == mo.cow_copies > 0
     assert mg.stats()["hits"] == mo.cache.hits
-    assert np.allclose(gm.kv_download(), kv, rtol=1e-4, atol=1e-5)
+    got = gm.kv_download()
+    assert np.max(np.abs(got - kv)) <= 1e-4 * np.max(np.abs(kv))
     gm.close()
