@@ -28,6 +28,9 @@ sys.path.insert(0, str(ROOT / "paged-infer_amd"))
 import pia  # noqa: E402
 
 METRIC = "int8 decode tok/s (B=1,32) + int8 GEMV HBM GB/s as % of ~8 TB/s peak"
+# HBM bytes per launch of the gate/up projection at batch 1, from rocprofv3 FETCH_SIZE and
+# WRITE_SIZE runs scaled by a 256 MiB copy (profiles/decode_b1_projection_traffic.md).
+TRAFFIC_GATE_UP_B1 = 23_420_000
 HBM_PEAK_GBS = 8000.0
 SEED = 2024
 
@@ -56,22 +59,26 @@ def decode_loop(model, toks, positions, tables, steps, bs, mgr=None):
 
 
 def profile_pass(model, toks, pos, tables, steps):
-    """Per-kernel-class device time of `steps` decode steps (HIP events around every launch on
-    the library's stream, eager launches behind a short device spin so the events bracket only
-    their kernel). Same inputs and kernels as the timed graph replays."""
+    """Per-class device time of `steps` decode steps: HIP events around every launch on the
+    library's stream (eager launches behind a short device spin so the host enqueues ahead and
+    each event pair brackets only its kernel). Same inputs and kernels as the timed replays."""
     model.profile(True)
-    acc = np.zeros(3)
-    by = np.zeros(3)
+    n = len(pia.Model.PROFILE_CLASSES)
+    acc, by, calls = np.zeros(n), np.zeros(n), np.zeros(n)
     for _ in range(steps):
         _, am = model.decode(toks, pos, tables, want_logits=False)
-        ms, b = model.profile_get()
+        ms, b, c = model.profile_get()
         acc += ms
         by += b
+        calls += c
         toks = am.tolist()
         pos = [p + 1 for p in pos]
     model.profile(False)
-    return dict(gemv_ms=acc[0] / steps, attn_ms=acc[1] / steps, other_ms=acc[2] / steps, gemv_bytes=by[0] / steps,
-                attn_bytes=by[1] / steps)
+    per = {name: {"ms_per_step": acc[i] / steps, "bytes_per_launch": by[i] / max(calls[i], 1),
+                  "us_per_launch": 1e3 * acc[i] / max(calls[i], 1), "launches_per_step": calls[i] / steps}
+           for i, name in enumerate(pia.Model.PROFILE_CLASSES)}
+    return dict(classes=per, gemv_ms=sum(acc[i] for i in range(5)) / steps, attn_ms=acc[5] / steps,
+                other_ms=acc[6] / steps, gemv_bytes=sum(by[i] for i in range(5)) / steps, attn_bytes=by[5] / steps)
 
 
 def run_b1(ctx, cfg, weights, steps, warmup, prompt_len=512):
@@ -130,12 +137,14 @@ def run_b32(ctx, cfg, weights, steps, warmup, batch=32):
     elapsed = time.perf_counter() - t0
     prof = profile_pass(model, toks, pos, tables, min(steps, 5))
     gemv_ms, attn_ms, gemv_bytes, attn_bytes = prof["gemv_ms"], prof["attn_ms"], prof["gemv_bytes"], prof["attn_bytes"]
+    gu = prof["classes"]["gate_up"]
     model.close()
     return dict(tok_s=batch * steps / elapsed, ms_per_step=1e3 * elapsed / steps,
                 prefill_tok_s=float(np.sum(ctxs)) / prefill_s, mean_ctx=float(np.mean(ctxs)),
                 gemv_gbs=(gemv_bytes / 1e9) / (gemv_ms / 1e3) if gemv_ms else None,
                 attn_gbs=(attn_bytes / 1e9) / (attn_ms / 1e3) if attn_ms else None,
-                gemv_ms=gemv_ms, attn_ms=attn_ms)
+                gemv_ms=gemv_ms, attn_ms=attn_ms,
+                gate_up_gbs=gu["bytes_per_launch"] / (gu["us_per_launch"] * 1e3))
 
 
 SWEEP_SHAPES = [  # (name, rows, cols) of the fused projections
@@ -190,6 +199,9 @@ def main():
     ap.add_argument("--no-b32", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep", action="store_true", help="also time each projection shape alone")
+    ap.add_argument("--only-b32", action="store_true", help="run only the batch-32 decode (profiling aid)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy one 256 MiB KV block 3 times (k_copy_block: known bytes, for PMC scaling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the int8 decode path is built and measured on a single MI355X; "
@@ -202,9 +214,24 @@ def main():
     log("building synthetic TinyLlama int8 weights")
     weights = pia.synth_weights(cfg, seed=SEED)
     ctx = pia.Context(0)
+    if args.copy_calibration:
+        lay = pia.KvLayout(1, 2, 32768, 8, 128)  # one block = 32768*8*2*128 floats = 256 MiB
+        buf = ctx.empty((2 * 32768 * 8 * 2 * 128,), np.float32)
+        for _ in range(3):
+            pia.check(pia.lib().pia_kv_copy_block_dev(ctx.h, buf.ptr, lay, 0, 1, None))
+        ctx.sync()
+        print(json.dumps({"copy_calibration": {"bytes_read": 1 << 28, "bytes_written": 1 << 28, "launches": 3}}))
+        return
+    if args.only_b32:
+        b32 = run_b32(ctx, cfg, weights, args.steps, args.warmup)
+        print(json.dumps({"b32": b32}), flush=True)
+        return
     log("B=1 decode")
     b1, kv_state = run_b1(ctx, cfg, weights, args.steps, args.warmup)
-    gemv_gbs = (b1["gemv_bytes"] / 1e9) / (b1["gemv_ms"] / 1e3)
+    # Dominant kernel of the step: the gate/up projection (largest share of the step's time).
+    dom = b1["classes"]["gate_up"]
+    dom_gbs = dom["bytes_per_launch"] / (dom["us_per_launch"] * 1e3)
+    agg_gbs = (b1["gemv_bytes"] / 1e9) / (b1["gemv_ms"] / 1e3)
     out = {
         "metric": METRIC,
         "value": round(b1["tok_s"], 2),
@@ -223,9 +250,13 @@ def main():
                    "weight_bytes": b1["weight_bytes"], "prefill_tok_s": round(b1["prefill_tok_s"], 1),
                    "gemv_ms_per_step": round(b1["gemv_ms"], 4), "attention_ms_per_step": round(b1["attn_ms"], 4),
                    "other_ms_per_step": round(b1["other_ms"], 4)},
-        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_gemv (all int8 projections + lm_head of a step, aggregated)"},
+        "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_GATE_UP_B1,
+                     "kernel": "k_gemv gate/up (11264 x 2048 int8, fused RMSNorm + SwiGLU), batch 1",
+                     "algorithmic_bytes_per_launch": int(dom["bytes_per_launch"]),
+                     "us_per_launch": round(dom["us_per_launch"], 3),
+                     "all_projections_gbs": round(agg_gbs, 1)},
+        "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in b1["classes"].items()},
     }
     if not args.no_b32:
         log("B=32 paged decode")

@@ -224,11 +224,15 @@ pia_status pia_model_decode(pia_model* m, const uint32_t* tokens, const int64_t*
 pia_status pia_model_prefill(pia_model* m, const uint32_t* tokens, int64_t n, int64_t start_pos,
                              const int32_t* table, int64_t table_len, float* logits, int32_t* argmax);
 
-/* Per-kernel timing of the last pia_model_decode / pia_model_prefill call (HIP events on the
- * context stream), accumulated per kernel class: 0 = int8 projections (GEMV/GEMM),
- * 1 = attention, 2 = everything else. Enable with pia_model_profile(m, 1). */
+/* Per-kernel timing of the last pia_model_decode / pia_model_prefill call (HIP events around
+ * every launch on the context stream), accumulated per class: 0 = q/k/v projection, 1 = o,
+ * 2 = gate/up, 3 = down, 4 = LM head, 5 = attention, 6 = everything else. `bytes` are the
+ * algorithmic bytes of those launches, `calls` their number. Enable with
+ * pia_model_profile(m, 1); profiled calls run without graph replay. No counterpart in the
+ * reference (its benches time whole steps). */
 pia_status pia_model_profile(pia_model* m, int32_t enable);
-pia_status pia_model_profile_get(pia_model* m, double* ms_per_class, int64_t* bytes_per_class, int32_t n_class);
+pia_status pia_model_profile_get(pia_model* m, double* ms_per_class, int64_t* bytes_per_class,
+                                 int64_t* calls_per_class, int32_t n_class);
 
 /* ------------------------------------------------------------------------------------ */
 /* Diagnostics (no counterpart in the reference).                                         */
@@ -238,8 +242,10 @@ pia_status pia_model_profile_get(pia_model* m, double* ms_per_class, int64_t* by
  * distinct weight copies (>= 1 GiB) that every launch streams from HBM, HIP events around a
  * replay; *us = mean microseconds per launch. Also reports the launch's
  * algorithmic bytes (int8 weights + scales + activations in + results out). */
-pia_status pia_bench_projection(pia_context* ctx, int64_t rows, int64_t cols, int64_t batch, int32_t reps, double* us,
-                                int64_t* bytes);
+/* flags: 1 = fused RMSNorm prologue, 2 = SwiGLU epilogue, 4 = residual-add epilogue,
+ * 8 = matrix-core path (digit split; the digit conversion is timed with it). */
+pia_status pia_bench_projection(pia_context* ctx, int64_t rows, int64_t cols, int64_t batch, int32_t reps,
+                                int32_t flags, double* us, int64_t* bytes);
 
 /* ------------------------------------------------------------------------------------ */
 /* Synthetic inputs (no counterpart in the reference: seeded data for tests and benches). */

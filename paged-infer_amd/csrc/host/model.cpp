@@ -23,6 +23,8 @@ inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
 // Rows up to which RMSNorm is fused into the projection that consumes it.
 constexpr int64_t kFusedNormRows = 64;
+// Batch from which int8 projections run on the matrix cores instead of the streaming GEMV.
+constexpr int64_t kMfmaMinBatch = 8;
 
 struct Proj {
   int kind = -1;  // -1 unset, 0 f32, 1 int8
@@ -47,8 +49,10 @@ struct Prof {
   std::vector<hipEvent_t> pool;
   std::vector<Rec> recs;
   size_t used = 0;
-  double ms[3] = {0, 0, 0};
-  int64_t bytes[3] = {0, 0, 0};
+  static constexpr int kClasses = 7;
+  double ms[kClasses] = {};
+  int64_t bytes[kClasses] = {};
+  int64_t calls[kClasses] = {};
 
   hipEvent_t ev() {
     if (used == pool.size()) {
@@ -89,7 +93,8 @@ struct pia_model {
   int64_t rope_len = 0;
 
   int64_t cap = 0;  // rows of activation scratch
-  DeviceBuffer x, xb, qkv, attn, h, logits, amax, attn_work, counters, step;
+  DeviceBuffer x, xb, qkv, attn, h, logits, amax, attn_work, step, xq;
+  int64_t mfma_min = kMfmaMinBatch;
   PinnedBuffer pin, pin_out;
   Prof prof;
 
@@ -138,11 +143,8 @@ struct pia_model {
     grow(qkv, c * ld_qkv * 4);
     grow(attn, c * ld_h * 4);
     grow(h, c * ld_i * 4);
-    grow(amax, c * 8);
-    if (static_cast<size_t>(c * cfg.kv_heads * 4) > counters.bytes) {
-      grow(counters, c * cfg.kv_heads * 4);
-      PIA_HIP(hipMemset(counters.ptr, 0, counters.bytes));
-    }
+    grow(amax, c * kArgmaxSlots * 8);
+    grow(xq, xdigits_bytes(c, std::max(cfg.hidden, cfg.inter)));
     cap = c;
   }
 
@@ -180,10 +182,32 @@ struct pia_model {
     return wb + 4 * batch * p.cols + 4 * batch * outr;
   }
 
+  // Profiling classes (pia_model_profile_get): projections by role, attention, the rest.
+  int proj_class(const Proj& p) const {
+    if (&p == &lm_head) return 4;
+    for (const auto& L : layers) {
+      if (&p == &L.qkv) return 0;
+      if (&p == &L.o) return 1;
+      if (&p == &L.gu) return 2;
+      if (&p == &L.down) return 3;
+    }
+    return 6;
+  }
+
   void gemv(const Proj& p, const float* x_in, int64_t ldx, const float* norm_w, float* out, int64_t ldo,
             int64_t batch, Epi epi, unsigned long long* amax_out = nullptr) {
+    const int cls = proj_class(p);
+    if (p.kind == 1 && batch >= mfma_min) {
+      timed(6, 0, [&] { launch_xdigits(x_in, ldx, norm_w, cfg.rms_eps, batch, p.cols, xq.ptr, st()); });
+      hipEvent_t b = nullptr;
+      begin(cls, proj_bytes(p, batch, epi), &b);
+      launch_gemm_i8_mfma(static_cast<const int8_t*>(p.w.ptr), p.ld, p.s.as<float>(), xq.ptr, out, ldo, 1, p.rows,
+                          p.cols, batch, epi, amax_out, st());
+      end(b);
+      return;
+    }
     hipEvent_t b = nullptr;
-    begin(0, proj_bytes(p, batch, epi), &b);
+    begin(cls, proj_bytes(p, batch, epi), &b);
     GemvArgs g{p.kind, p.w.ptr, p.ld, p.kind == 1 ? p.s.as<float>() : nullptr, x_in, ldx, norm_w, cfg.rms_eps,
                out, ldo, 1, p.rows, p.cols, batch, epi, amax_out};
     launch_gemv(g, st());
@@ -194,10 +218,10 @@ struct pia_model {
   // a separate normalization pass into xb for large ones.
   void normed_gemv(const Proj& p, const float* X, const float* norm_w, int64_t n, float* out, int64_t ldo, Epi epi,
                    unsigned long long* amax_out = nullptr) {
-    if (n <= kFusedNormRows) {
+    if (n <= kFusedNormRows || (p.kind == 1 && n >= mfma_min)) {
       gemv(p, X, ld_h, norm_w, out, ldo, n, epi, amax_out);
     } else {
-      timed(2, 0, [&] { launch_rmsnorm(X, ld_h, norm_w, xb.as<float>(), ld_h, n, cfg.hidden, cfg.rms_eps, st()); });
+      timed(6, 0, [&] { launch_rmsnorm(X, ld_h, norm_w, xb.as<float>(), ld_h, n, cfg.hidden, cfg.rms_eps, st()); });
       gemv(p, xb.as<float>(), ld_h, nullptr, out, ldo, n, epi, amax_out);
     }
   }
@@ -228,18 +252,18 @@ struct pia_model {
     float* QKV = qkv.as<float>();
     float* ATT = attn.as<float>();
     float* H = h.as<float>();
-    timed(2, 0, [&] {
+    timed(6, 0, [&] {
       launch_embed(in.tokens, embed.as<uint16_t>(), X, ld_h, n, c.hidden, c.vocab, amax.as<unsigned long long>(), st());
     });
     for (int64_t l = 0; l < c.layers; ++l) {
       Layer& L = layers[l];
       normed_gemv(L.qkv, X, L.attn_norm.as<float>(), n, QKV, ld_qkv, Epi::Store);
-      timed(1, attn_bytes, [&] {
+      timed(5, attn_bytes, [&] {
         if (!fused)
           launch_rope_kv_write(QKV, ld_qkv, in.entries, in.tables, rope_cos.as<float>(), rope_sin.as<float>(),
                                kv.as<float>(), layout, c.heads, n, l, st());
         AttnLaunch a{QKV, ld_qkv, ATT, ld_h, kv.as<float>(), &layout, c.heads, in.entries, in.tables, n, l, plan,
-                     attn_work.ptr, counters.as<int>(), fused, rope_cos.as<float>(), rope_sin.as<float>()};
+                     attn_work.ptr, fused, rope_cos.as<float>(), rope_sin.as<float>()};
         launch_attention(a, st());
       });
       gemv(L.o, ATT, ld_h, nullptr, X, ld_h, n, Epi::Add);
@@ -248,18 +272,24 @@ struct pia_model {
     }
   }
 
-  // Copy the fused-argmax slots back (the low 32 bits are the row) and wait for the step.
+  // Copy the fused-argmax slots back, take the max of each row's slots (the low 32 bits are
+  // the winning row) and wait for the step.
   void read_argmax(int32_t* out, int64_t batch) {
-    pin_out.ensure(batch * 8);
-    PIA_HIP(hipMemcpyAsync(pin_out.ptr, amax.ptr, batch * 8, hipMemcpyDeviceToHost, st()));
+    const size_t bytes = batch * kArgmaxSlots * 8;
+    pin_out.ensure(bytes);
+    PIA_HIP(hipMemcpyAsync(pin_out.ptr, amax.ptr, bytes, hipMemcpyDeviceToHost, st()));
     PIA_HIP(hipStreamSynchronize(st()));
     const auto* v = static_cast<const unsigned long long*>(pin_out.ptr);
     if (out)
-      for (int64_t b = 0; b < batch; ++b) out[b] = static_cast<int32_t>(v[b] & 0xffffffffull);
+      for (int64_t b = 0; b < batch; ++b) {
+        unsigned long long best = 0;
+        for (int i = 0; i < kArgmaxSlots; ++i) best = std::max(best, v[b * kArgmaxSlots + i]);
+        out[b] = static_cast<int32_t>(best & 0xffffffffull);
+      }
   }
 
   void finish_prof() {
-    for (int i = 0; i < 3; ++i) prof.ms[i] = 0, prof.bytes[i] = 0;
+    for (int i = 0; i < Prof::kClasses; ++i) prof.ms[i] = 0, prof.bytes[i] = 0, prof.calls[i] = 0;
     if (!prof.on) return;
     PIA_HIP(hipStreamSynchronize(st()));
     for (auto& r : prof.recs) {
@@ -267,14 +297,20 @@ struct pia_model {
       PIA_HIP(hipEventElapsedTime(&t, r.a, r.b));
       prof.ms[r.cls] += t;
       prof.bytes[r.cls] += r.bytes;
+      prof.calls[r.cls] += 1;
     }
     prof.reset();
   }
 
-  // Run `body` eagerly (profiling: a short device spin first lets the host enqueue ahead, so
-  // each kernel's events bracket only that kernel), or through a cached graph for `key`.
+  // Run `body` eagerly (one-shot calls such as prefill; profiling, where a short device spin
+  // first lets the host enqueue ahead so each kernel's events bracket only that kernel), or
+  // through a cached graph for `key` (decode steps, replayed every step).
   template <typename F>
-  void run_step(const std::array<int64_t, 6>& key, F&& body) {
+  void run_step(const std::array<int64_t, 6>& key, bool replay, F&& body) {
+    if (!replay && !prof.on) {
+      body();
+      return;
+    }
     if (prof.on) {
       prof.reset();
       launch_spin(3000.0, st());
@@ -309,7 +345,7 @@ void alloc_proj(Proj& p, int kind, int64_t rows, int64_t cols) {
   p.kind = kind;
   p.rows = rows;
   p.cols = cols;
-  p.ld = round_up(cols, kind == 1 ? 16 : 4);
+  p.ld = round_up(cols, kind == 1 ? 64 : 4);  // int8 rows: whole 64-byte MFMA k-steps
   const int64_t esz = kind == 1 ? 1 : 4;
   p.w.ensure(rows * p.ld * esz);
   PIA_HIP(hipMemset(p.w.ptr, 0, rows * p.ld * esz));
@@ -492,12 +528,13 @@ pia_status pia_model_profile(pia_model* m, int32_t enable) {
   PIA_API_END
 }
 
-pia_status pia_model_profile_get(pia_model* m, double* ms, int64_t* bytes, int32_t n) {
+pia_status pia_model_profile_get(pia_model* m, double* ms, int64_t* bytes, int64_t* calls, int32_t n) {
   PIA_API_BEGIN
   PIA_REQUIRE(m, "null model");
-  for (int i = 0; i < n && i < 3; ++i) {
+  for (int i = 0; i < n && i < Prof::kClasses; ++i) {
     if (ms) ms[i] = m->prof.ms[i];
     if (bytes) bytes[i] = m->prof.bytes[i];
+    if (calls) calls[i] = m->prof.calls[i];
   }
   PIA_API_END
 }
@@ -600,7 +637,7 @@ pia_status pia_model_decode(pia_model* m, const uint32_t* tokens, const int64_t*
   const int64_t wb = attention_work_bytes(batch, c.heads, m->hd, plan.splits);
   if (wb) m->grow(m->attn_work, wb);
   const pia_model::StepDev in = upload_step(m, tok, ent, tables, ntab);
-  m->run_step({0, batch, plan.split, plan.splits, fused ? 1 : 0, 0}, [&] {
+  m->run_step({0, batch, plan.split, plan.splits, plan.chunk, fused ? 1 : 0}, true, [&] {
     m->run_layers(batch, in, plan, fused, mapped);
     m->normed_gemv(m->lm_head, m->x.as<float>(), m->final_norm.as<float>(), batch, m->logits.as<float>(), m->ld_v,
                    Epi::Store, m->amax.as<unsigned long long>());
@@ -644,7 +681,7 @@ pia_status pia_model_prefill(pia_model* m, const uint32_t* tokens, int64_t n, in
   const int64_t wb = attention_work_bytes(n, c.heads, m->hd, plan.splits);
   if (wb) m->grow(m->attn_work, wb);
   const pia_model::StepDev in = upload_step(m, tok, ent, table, table_len);
-  m->run_step({1, n, plan.split, plan.splits, fused ? 1 : 0, 0}, [&] {
+  m->run_step({1, n, plan.split, plan.splits, plan.chunk, fused ? 1 : 0}, false, [&] {
     m->run_layers(n, in, plan, fused, mapped);
     // Only the last position pays for the LM head (src/model.rs:1249-1254).
     m->normed_gemv(m->lm_head, m->x.as<float>() + (n - 1) * m->ld_h, m->final_norm.as<float>(), 1,

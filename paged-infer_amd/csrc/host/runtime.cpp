@@ -264,15 +264,11 @@ pia_status pia_paged_attention_dev(pia_context* ctx, float* out, const float* q,
   }
   const int64_t hd = layout->head_dim;
   const AttnPlan plan = plan_attention(n, layout->num_kv_heads, hd, widest, ctx->num_cus);
-  DeviceBuffer work, counters;
+  DeviceBuffer work;
   const int64_t wb = attention_work_bytes(n, num_heads, hd, plan.splits);
-  if (wb) {
-    work.ensure(wb);
-    counters.ensure(n * layout->num_kv_heads * sizeof(int));
-    PIA_HIP(hipMemsetAsync(counters.ptr, 0, counters.bytes, st));
-  }
+  if (wb) work.ensure(wb);
   AttnLaunch a{q, num_heads * hd, out, num_heads * hd, const_cast<float*>(kv), layout, num_heads, entries, tables,
-               n, layer, plan, work.ptr, counters.as<int>(), false, nullptr, nullptr};
+               n, layer, plan, work.ptr, false, nullptr, nullptr};
   launch_attention(a, st);
   PIA_HIP(hipStreamSynchronize(st));
   PIA_API_END
@@ -295,22 +291,25 @@ pia_status pia_argmax_dev(pia_context* ctx, int32_t* out, const float* logits, i
   PIA_API_END
 }
 
-pia_status pia_bench_projection(pia_context* ctx, int64_t rows, int64_t cols, int64_t batch, int32_t reps, double* us,
-                                int64_t* bytes) {
+pia_status pia_bench_projection(pia_context* ctx, int64_t rows, int64_t cols, int64_t batch, int32_t reps,
+                                int32_t flags, double* us, int64_t* bytes) {
   PIA_API_BEGIN
   PIA_REQUIRE(ctx && us && bytes, "null argument");
   PIA_REQUIRE(rows > 0 && cols > 0 && batch > 0 && reps > 0 && reps <= 1000, "bad benchmark shape");
   PIA_HIP(hipSetDevice(ctx->device));
-  const int64_t ldw = (cols + 15) / 16 * 16, ldx = (cols + 15) / 16 * 16;
+  PIA_REQUIRE(!(flags & 2) || rows % 2 == 0, "SwiGLU needs an even row count");
+  const int64_t ldw = (cols + 63) / 64 * 64, ldx = (cols + 15) / 16 * 16;
   // Enough distinct weight copies (>= 1 GiB in total) that consecutive launches stream from
   // HBM instead of hitting the 256 MB Infinity Cache.
   const int64_t wbytes = rows * ldw;
   const int ncopy = static_cast<int>(std::min<int64_t>(64, std::max<int64_t>(2, ((int64_t(1) << 30) + wbytes - 1) / wbytes)));
-  DeviceBuffer w, s, x, y;
+  DeviceBuffer w, s, x, y, nw, xq;
   w.ensure(wbytes * ncopy);
   s.ensure(rows * 4);
   x.ensure(batch * ldx * 4);
   y.ensure(batch * rows * 4);
+  nw.ensure(ldx * 4);
+  xq.ensure(xdigits_bytes(batch, cols));
   {
     std::vector<int8_t> hw(wbytes);
     for (size_t i = 0; i < hw.size(); ++i) hw[i] = static_cast<int8_t>((i * 2654435761u >> 13) % 255 - 127);
@@ -320,17 +319,28 @@ pia_status pia_bench_projection(pia_context* ctx, int64_t rows, int64_t cols, in
     for (size_t i = 0; i < hx.size(); ++i) hx[i] = static_cast<float>((i * 40503u) % 2001) / 1000.0f - 1.0f;
     PIA_HIP(hipMemcpy(s.ptr, hs.data(), hs.size() * 4, hipMemcpyHostToDevice));
     PIA_HIP(hipMemcpy(x.ptr, hx.data(), hx.size() * 4, hipMemcpyHostToDevice));
+    std::vector<float> hn(ldx, 1.0f);
+    PIA_HIP(hipMemcpy(nw.ptr, hn.data(), hn.size() * 4, hipMemcpyHostToDevice));
   }
-  auto args = [&](int i) {
-    return GemvArgs{1, static_cast<int8_t*>(w.ptr) + (i % ncopy) * wbytes, ldw, s.as<float>(), x.as<float>(), ldx,
-                    nullptr, 0.f, y.as<float>(), rows, 1, rows, cols, batch, Epi::Store};
-  };
+  const Epi epi = (flags & 2) ? Epi::Swiglu : (flags & 4) ? Epi::Add : Epi::Store;
+  const float* norm = (flags & 1) ? nw.as<float>() : nullptr;
   hipStream_t st = ctx->stream;
-  launch_gemv(args(0), st);
+  auto one = [&](int i) {
+    const int8_t* wi = static_cast<int8_t*>(w.ptr) + (i % ncopy) * wbytes;
+    if (flags & 8) {
+      launch_xdigits(x.as<float>(), ldx, norm, 1e-5f, batch, cols, xq.ptr, st);
+      launch_gemm_i8_mfma(wi, ldw, s.as<float>(), xq.ptr, y.as<float>(), rows, 1, rows, cols, batch, epi, nullptr, st);
+    } else {
+      launch_gemv(GemvArgs{1, wi, ldw, s.as<float>(), x.as<float>(), ldx, norm, 1e-5f, y.as<float>(), rows, 1, rows,
+                           cols, batch, epi},
+                  st);
+    }
+  };
+  one(0);
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   PIA_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
-  for (int i = 0; i < reps; ++i) launch_gemv(args(i + 1), st);
+  for (int i = 0; i < reps; ++i) one(i + 1);
   PIA_HIP(hipStreamEndCapture(st, &graph));
   PIA_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
   hipEvent_t e0, e1;

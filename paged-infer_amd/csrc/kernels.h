@@ -11,6 +11,10 @@
 
 namespace pia {
 
+// Slots per batch row of the fused argmax: spreading the atomics over 64 addresses keeps
+// thousands of workgroups from serializing on one.
+constexpr int kArgmaxSlots = 64;
+
 // Epilogue of a projection: store, accumulate into the destination (residual add, as
 // src/model.rs:1127-1129 and :1165-1167 do with proj_out / ff_down), or SwiGLU over
 // interleaved gate/up row pairs (src/math.rs:293-302).
@@ -33,27 +37,31 @@ struct GemvArgs {
   int64_t osb, osr;
   int64_t rows, cols, batch;
   Epi epi;
-  // Optional fused greedy argmax (Store only): amax[b] = max over rows of
-  // (f32 total-order key of out[b][r]) << 32 | r; the caller zeroes amax first.
+  // Optional fused greedy argmax (Store only): the max over rows of
+  // (f32 total-order key of out[b][r]) << 32 | r lands in one of the kArgmaxSlots slots
+  // amax[b * kArgmaxSlots + i]; the caller zeroes them first and takes the max of the slots.
   unsigned long long* amax = nullptr;
 };
 void launch_gemv(const GemvArgs& args, hipStream_t st);
 
-// Batched int8 projection on MFMA for batch >= 16 (decode batches and prefill).
-// Activations are split into three signed 8-bit digits per row (exact for the 23-bit
-// fixed-point image of x); weights stay int8; accumulation is exact int32.
-// `xq` workspace: see xdigits_bytes(). out[b*osb + r*osr] (=|+=) as launch_gemv.
+// Batched int8 projection on the int8 matrix cores (see gemm_mfma.hip). launch_xdigits writes
+// the activations (optionally RMSNorm(x) * norm_w) as three signed 8-bit digits of a 23-bit
+// fixed-point image per row into the workspace `xq` (xdigits_bytes); launch_gemm_i8_mfma then
+// computes the projection with exact int32 accumulation and the epilogues of launch_gemv.
+// Weight rows must be zero-padded to a multiple of 64 bytes (ldw >= that).
 int64_t xdigits_bytes(int64_t batch, int64_t cols);
-void launch_xdigits(const float* x, int64_t ldx, int64_t batch, int64_t cols, void* xq, hipStream_t st);
+void launch_xdigits(const float* x, int64_t ldx, const float* norm_w, float eps, int64_t batch, int64_t cols,
+                    void* xq, hipStream_t st);
 void launch_gemm_i8_mfma(const int8_t* W, int64_t ldw, const float* scales, const void* xq, float* out, int64_t osb,
-                         int64_t osr, int64_t rows, int64_t cols, int64_t batch, Epi epi, hipStream_t st);
+                         int64_t osr, int64_t rows, int64_t cols, int64_t batch, Epi epi, unsigned long long* amax,
+                         hipStream_t st);
 
 // out[r] = RMSNorm(x[r]) * w  (src/math.rs:4-22), rows of n, row strides ldx / ldo.
 void launch_rmsnorm(const float* x, int64_t ldx, const float* w, float* out, int64_t ldo, int64_t rows, int64_t n,
                     float eps, hipStream_t st);
 
 // x[b] = bf16 embedding row (tokens[b] % vocab) widened to f32 (src/model.rs:1015-1020).
-// Also zeroes amax[0..batch) (the fused-argmax slots of this step) when amax is given.
+// Also zeroes amax[0 .. batch * kArgmaxSlots) (this step's fused-argmax slots) when given.
 void launch_embed(const int32_t* tokens, const uint16_t* embed, float* x, int64_t ldx, int64_t batch, int64_t hidden,
                   int64_t vocab, unsigned long long* amax, hipStream_t st);
 
@@ -65,13 +73,14 @@ void launch_rope_kv_write(float* qkv, int64_t ldq, const pia_attn_entry* entries
                           int64_t heads, int64_t batch, int64_t layer, hipStream_t st);
 
 // PagedAttention::run for one layer (see attention.hip). `plan` picks the token split;
-// `work` (attention_work_bytes) and `counters` (n * num_kv_heads ints, zero between launches)
-// are needed when plan.splits > 1. When `fused`, q rows are the raw qkv rows (RoPE applied in
-// the kernel) and each entry's own K/V is rotated and written by the kernel; only valid when
-// no entry reads a cache slot written by another entry of the same launch.
+// `work` (attention_work_bytes) is needed when plan.splits > 1 (a combine kernel follows).
+// When `fused`, q rows are the raw qkv rows (RoPE applied in the kernel) and each entry's own
+// K/V is rotated and written by the kernel; only valid when no entry reads a cache slot
+// written by another entry of the same launch.
 struct AttnPlan {
-  int64_t split;   // tokens per workgroup: 256, 128 or 64
-  int64_t splits;  // workgroups per (entry, kv head)
+  int64_t split;   // tokens per workgroup (a multiple of chunk)
+  int64_t splits;  // workgroups per (entry, kv head), <= 128
+  int64_t chunk;   // tokens per inner step: 256, 128 or 64
 };
 AttnPlan plan_attention(int64_t n, int64_t num_kv_heads, int64_t head_dim, int64_t max_window, int num_cus);
 int64_t attention_work_bytes(int64_t n, int64_t heads, int64_t head_dim, int64_t splits);
@@ -88,7 +97,6 @@ struct AttnLaunch {
   int64_t n, layer;
   AttnPlan plan;
   void* work;
-  int* counters;
   bool fused;
   const float* rope_cos;
   const float* rope_sin;

@@ -14,6 +14,7 @@
 // position, rotates k, writes k and v into the cache and uses them straight from LDS
 // (src/model.rs:1068-1107 then :1111-1118), so a decode layer's attention is one launch.
 #include <cfloat>
+#include <cstdlib>
 
 #include "common.h"
 #include "kernels.h"
@@ -46,50 +47,43 @@ struct AttnParams {
   float scale;
   const pia_attn_entry* entries;
   const int32_t* tables;
-  int split, nsplit;
+  int split, nsplit, chunk;
   float* part_o;
   float* part_ml;
-  int* counters;  // [n][hkv], zero between launches
   const float* rope_cos;
   const float* rope_sin;
 };
 
 // HD: compile-time head_dim (0 = runtime p.hd, for unusual shapes); every loop over the head
-// dimension and over the tokens of a split issues its loads before their first use.
+// dimension and over the tokens of a chunk issues its loads before their first use.
+//
+// A workgroup owns the tokens [t0, t1) of one (entry, kv head): the whole window when
+// p.nsplit == 1, else one split. It walks them in chunks of 256 / TPT tokens with a running
+// (online) softmax: per chunk the new maximum rescales the running sum and the V accumulators.
 template <int G, int HD, int TPT, bool FUSED>
 __global__ __launch_bounds__(kThreads) void k_attn(AttnParams p) {
   extern __shared__ float smem[];
   const int hd = HD ? HD : p.hd;
+  constexpr int kChunk = kThreads / TPT;                    // tokens per chunk
   float* qs = smem;                                         // [G][hd]
-  float* sc = qs + G * hd;                                  // [G][kThreads]
-  float* stat = sc + G * kThreads;                          // [G][2]
-  float* knew = stat + 2 * G;                               // [hd]  (fused: this entry's k)
+  float* sc = qs + G * hd;                                  // [G][kChunk]
+  float* stat = sc + G * kChunk;                            // [G][4]: m, l, alpha, -
+  float* knew = stat + 4 * G;                               // [hd]  (fused: this entry's k)
   float* vnew = knew + hd;                                  // [hd]
-  int* slot_of = reinterpret_cast<int*>(vnew + hd);         // [kThreads]
-  int* flag = slot_of + kThreads;                           // [1]
-  float* red = reinterpret_cast<float*>(flag + 1);          // [ngrp][G][hd]
+  int* slot_of = reinterpret_cast<int*>(vnew + hd);         // [kChunk]
+  float* red = reinterpret_cast<float*>(slot_of + kChunk);  // [ngrp][G][hd]
 
   const int s = blockIdx.x, kvh = blockIdx.y, e = blockIdx.z;
   const int tid = threadIdx.x;
   const pia_attn_entry en = p.entries[e];
   const int t0 = en.start + s * p.split;
   const int t1 = min(en.pos + 1, t0 + p.split);
-  const int count = max(0, t1 - t0);
   const int half = hd / 2;
   const float* qrow = p.q + static_cast<int64_t>(e) * p.ldq;
-  const bool own = FUSED && en.pos >= t0 && en.pos < t1;  // this split holds the entry's token
+  const bool own = FUSED && en.pos >= t0 && en.pos < t1;  // this workgroup holds the entry's token
   const int64_t kv_head_stride = 2 * static_cast<int64_t>(hd);
   auto kv_at = [&](int slot) { return p.kv + ((p.layer_slots + slot) * p.hkv + kvh) * kv_head_stride; };
 
-  {
-    int slot = -1;
-    if (tid < count) {
-      const int t = t0 + tid;
-      const int lb = t / p.block_size;
-      if (lb < en.table_len) slot = p.tables[en.table_off + lb] * p.block_size + (t % p.block_size);
-    }
-    slot_of[tid] = slot;
-  }
   if (FUSED) {
     const float* c = p.rope_cos + static_cast<int64_t>(en.pos) * half;
     const float* sn = p.rope_sin + static_cast<int64_t>(en.pos) * half;
@@ -123,98 +117,118 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnParams p) {
   } else {
     for (int i = tid; i < G * hd; i += kThreads) qs[i] = qrow[kvh * G * hd + i];
   }
-  __syncthreads();
+  if (tid < G) {
+    stat[4 * tid] = -INFINITY;
+    stat[4 * tid + 1] = 0.0f;
+  }
 
-  // Scores: TPT threads per token, each covering hd / TPT dims, reduced by lane shuffles.
-  {
-    const int tok = tid / TPT, part = tid % TPT;
-    const int seg = hd / TPT;
-    const int slot = tok < count ? slot_of[tok] : -1;
-    float acc[G];
+  const int tpg = hd / 4;
+  const int ngrp = kThreads / tpg;
+  const int grp = tid / tpg, d4 = (tid % tpg) * 4;
+  float o[G][4];
 #pragma unroll
-    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
-    if (slot >= 0) {
-      const float* kp = (FUSED && own && t0 + tok == en.pos) ? knew : kv_at(slot);
-      kp += part * seg;
-      const float* qp = qs + part * seg;
-      if constexpr (HD != 0) {
-        constexpr int kSeg = HD / TPT;
-        float4 k4[kSeg / 4];
+  for (int g = 0; g < G; ++g) o[g][0] = o[g][1] = o[g][2] = o[g][3] = 0.0f;
+
+  for (int c0 = t0; c0 < t1; c0 += kChunk) {
+    const int count = min(kChunk, t1 - c0);
+    if (tid < kChunk) {
+      int slot = -1;
+      if (tid < count) {
+        const int t = c0 + tid;
+        const int lb = t / p.block_size;
+        if (lb < en.table_len) slot = p.tables[en.table_off + lb] * p.block_size + (t % p.block_size);
+      }
+      slot_of[tid] = slot;
+    }
+    __syncthreads();
+
+    // Scores: TPT threads per token, each covering hd / TPT dims, reduced by lane shuffles.
+    {
+      const int tok = tid / TPT, part = tid % TPT;
+      const int seg = hd / TPT;
+      const int slot = tok < count ? slot_of[tok] : -1;
+      float acc[G];
 #pragma unroll
-        for (int i = 0; i < kSeg / 4; ++i) k4[i] = reinterpret_cast<const float4*>(kp)[i];
+      for (int g = 0; g < G; ++g) acc[g] = 0.0f;
+      if (slot >= 0) {
+        const float* kp = (FUSED && own && c0 + tok == en.pos) ? knew : kv_at(slot);
+        kp += part * seg;
+        const float* qp = qs + part * seg;
+        if constexpr (HD != 0) {
+          constexpr int kSeg = HD / TPT;
+          float4 k4[kSeg / 4];
 #pragma unroll
-        for (int i = 0; i < kSeg / 4; ++i)
+          for (int i = 0; i < kSeg / 4; ++i) k4[i] = reinterpret_cast<const float4*>(kp)[i];
 #pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const float4 q4 = reinterpret_cast<const float4*>(qp + g * HD)[i];
-            acc[g] = __builtin_fmaf(q4.x, k4[i].x, acc[g]);
-            acc[g] = __builtin_fmaf(q4.y, k4[i].y, acc[g]);
-            acc[g] = __builtin_fmaf(q4.z, k4[i].z, acc[g]);
-            acc[g] = __builtin_fmaf(q4.w, k4[i].w, acc[g]);
-          }
-      } else {
-        for (int d = 0; d < seg; d += 4) {
-          const float4 k4 = *reinterpret_cast<const float4*>(kp + d);
+          for (int i = 0; i < kSeg / 4; ++i)
 #pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const float* qg = qp + g * hd + d;
-            acc[g] = __builtin_fmaf(qg[0], k4.x, acc[g]);
-            acc[g] = __builtin_fmaf(qg[1], k4.y, acc[g]);
-            acc[g] = __builtin_fmaf(qg[2], k4.z, acc[g]);
-            acc[g] = __builtin_fmaf(qg[3], k4.w, acc[g]);
+            for (int g = 0; g < G; ++g) {
+              const float4 q4 = reinterpret_cast<const float4*>(qp + g * HD)[i];
+              acc[g] = __builtin_fmaf(q4.x, k4[i].x, acc[g]);
+              acc[g] = __builtin_fmaf(q4.y, k4[i].y, acc[g]);
+              acc[g] = __builtin_fmaf(q4.z, k4[i].z, acc[g]);
+              acc[g] = __builtin_fmaf(q4.w, k4[i].w, acc[g]);
+            }
+        } else {
+          for (int d = 0; d < seg; d += 4) {
+            const float4 k4 = *reinterpret_cast<const float4*>(kp + d);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              const float* qg = qp + g * hd + d;
+              acc[g] = __builtin_fmaf(qg[0], k4.x, acc[g]);
+              acc[g] = __builtin_fmaf(qg[1], k4.y, acc[g]);
+              acc[g] = __builtin_fmaf(qg[2], k4.z, acc[g]);
+              acc[g] = __builtin_fmaf(qg[3], k4.w, acc[g]);
+            }
           }
         }
       }
-    }
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+      for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int off = TPT / 2; off >= 1; off >>= 1) acc[g] += __shfl_xor(acc[g], off, 64);
-    if (part == 0 && tok < p.split) {
+        for (int off = TPT / 2; off >= 1; off >>= 1) acc[g] += __shfl_xor(acc[g], off, 64);
+      if (part == 0) {
 #pragma unroll
-      for (int g = 0; g < G; ++g) sc[g * kThreads + tok] = slot >= 0 ? acc[g] * p.scale : -INFINITY;
-    }
-    for (int i = p.split + tid; i < kThreads; i += kThreads)
-#pragma unroll
-      for (int g = 0; g < G; ++g) sc[g * kThreads + i] = -INFINITY;
-  }
-  __syncthreads();
-
-  // Per-head max and sum of exp over this split (one wavefront per head, round robin).
-  {
-    const int wave = tid >> 6, lane = tid & 63;
-    for (int g = wave; g < G; g += kThreads / 64) {
-      float* row = sc + g * kThreads;
-      float m = -INFINITY;
-#pragma unroll
-      for (int i = lane; i < kThreads; i += 64) m = fmaxf(m, row[i]);
-      m = wave_max(m);
-      float l = 0.0f;
-#pragma unroll
-      for (int i = lane; i < kThreads; i += 64) {
-        const float pr = (m == -INFINITY) ? 0.0f : expf(row[i] - m);
-        row[i] = pr;
-        l += pr;
-      }
-      l = wave_sum(l);
-      if (lane == 0) {
-        stat[2 * g] = m;
-        stat[2 * g + 1] = l;
+        for (int g = 0; g < G; ++g) sc[g * kChunk + tok] = slot >= 0 ? acc[g] * p.scale : -INFINITY;
       }
     }
-  }
-  __syncthreads();
+    __syncthreads();
 
-  // V accumulation: hd/4 threads per token group, each owning 4 consecutive dims; 4 tokens'
-  // loads in flight per thread.
-  const int tpg = hd / 4;
-  const int ngrp = kThreads / tpg;
-  {
-    const int grp = tid / tpg, d4 = (tid % tpg) * 4;
+    // Running max / sum per head (one wavefront per head, round robin); sc becomes p.
+    {
+      const int wave = tid >> 6, lane = tid & 63;
+      for (int g = wave; g < G; g += kThreads / 64) {
+        float* row = sc + g * kChunk;
+        float m = -INFINITY;
+        for (int i = lane; i < kChunk; i += 64) m = fmaxf(m, row[i]);
+        m = wave_max(m);
+        const float m_old = stat[4 * g];
+        const float m_new = fmaxf(m_old, m);
+        float l = 0.0f;
+        for (int i = lane; i < kChunk; i += 64) {
+          const float pr = (m_new == -INFINITY) ? 0.0f : expf(row[i] - m_new);
+          row[i] = pr;
+          l += pr;
+        }
+        l = wave_sum(l);
+        if (lane == 0) {
+          const float alpha = (m_old == -INFINITY) ? 0.0f : expf(m_old - m_new);
+          stat[4 * g] = m_new;
+          stat[4 * g + 1] = __builtin_fmaf(stat[4 * g + 1], alpha, l);
+          stat[4 * g + 2] = alpha;
+        }
+      }
+    }
+    __syncthreads();
+
+    // V accumulation: hd/4 threads per token group, 4 consecutive dims each; 4 tokens' loads
+    // in flight per thread.
     if (grp < ngrp) {
-      float o[G][4];
 #pragma unroll
-      for (int g = 0; g < G; ++g) o[g][0] = o[g][1] = o[g][2] = o[g][3] = 0.0f;
+      for (int g = 0; g < G; ++g) {
+        const float alpha = stat[4 * g + 2];
+        o[g][0] *= alpha, o[g][1] *= alpha, o[g][2] *= alpha, o[g][3] *= alpha;
+      }
       for (int i0 = grp; i0 < count; i0 += 4 * ngrp) {
         float4 v4[4];
         int idx[4];
@@ -224,7 +238,7 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnParams p) {
           const int slot = i < count ? slot_of[i] : -1;
           idx[u] = slot >= 0 ? i : -1;
           if (slot >= 0) {
-            const float* vp = (FUSED && own && t0 + i == en.pos) ? vnew : kv_at(slot) + hd;
+            const float* vp = (FUSED && own && c0 + i == en.pos) ? vnew : kv_at(slot) + hd;
             v4[u] = *reinterpret_cast<const float4*>(vp + d4);
           } else {
             v4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -235,7 +249,7 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnParams p) {
           if (idx[u] < 0) continue;
 #pragma unroll
           for (int g = 0; g < G; ++g) {
-            const float pr = sc[g * kThreads + idx[u]];
+            const float pr = sc[g * kChunk + idx[u]];
             o[g][0] = __builtin_fmaf(pr, v4[u].x, o[g][0]);
             o[g][1] = __builtin_fmaf(pr, v4[u].y, o[g][1]);
             o[g][2] = __builtin_fmaf(pr, v4[u].z, o[g][2]);
@@ -243,95 +257,84 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnParams p) {
           }
         }
       }
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) red[(grp * G + g) * hd + d4 + j] = o[g][j];
     }
+    __syncthreads();  // slot_of / sc are rewritten by the next chunk
+  }
+
+  if (grp < ngrp) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[(grp * G + g) * hd + d4 + j] = o[g][j];
   }
   __syncthreads();
-
   for (int idx = tid; idx < G * hd; idx += kThreads) {
     float acc = 0.0f;
     for (int gr = 0; gr < ngrp; ++gr) acc += red[gr * G * hd + idx];
     const int g = idx / hd, d = idx % hd;
     const int h = kvh * G + g;
     if (p.nsplit == 1) {
-      const float l = stat[2 * g + 1];
+      const float l = stat[4 * g + 1];
       p.out[static_cast<int64_t>(e) * p.ldo + h * hd + d] = l > 0.0f ? acc / l : 0.0f;
     } else {
       const int64_t ps = (static_cast<int64_t>(e) * p.heads + h) * p.nsplit + s;
       p.part_o[ps * hd + d] = acc;
       if (d == 0) {
-        p.part_ml[2 * ps] = stat[2 * g];
-        p.part_ml[2 * ps + 1] = stat[2 * g + 1];
+        p.part_ml[2 * ps] = stat[4 * g];
+        p.part_ml[2 * ps + 1] = stat[4 * g + 1];
       }
     }
   }
-  if (p.nsplit == 1) return;
-
-  // The last split of this (entry, kv head) to finish combines all of them.
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const int prev = atomicAdd(&p.counters[e * p.hkv + kvh], 1);
-    flag[0] = prev == p.nsplit - 1;
-  }
-  __syncthreads();
-  if (!flag[0]) return;
-  __threadfence();
-  const int ns = p.nsplit;
-  const int64_t head0 = static_cast<int64_t>(e) * p.heads + kvh * G;
-  // Split weights exp(m_k - M) / L per head, staged in LDS (sc holds G * kThreads floats).
-  float* wk = sc;  // [G][ns], ns <= kThreads / 2 (launch_attention guarantees it)
-  for (int i = tid; i < G * ns; i += kThreads) {
-    const int g = i / ns, k = i % ns;
-    wk[i] = __builtin_nontemporal_load(&p.part_ml[2 * ((head0 + g) * ns + k)]);
-    wk[G * ns + i] = __builtin_nontemporal_load(&p.part_ml[2 * ((head0 + g) * ns + k) + 1]);
-  }
-  __syncthreads();
-  {
-    const int wave = tid >> 6, lane = tid & 63;
-    for (int g = wave; g < G; g += kThreads / 64) {
-      float m = -INFINITY;
-      for (int k = lane; k < ns; k += 64) m = fmaxf(m, wk[g * ns + k]);
-      m = wave_max(m);
-      float l = 0.0f;
-      for (int k = lane; k < ns; k += 64) {
-        const float mk = wk[g * ns + k];
-        if (mk != -INFINITY) l = __builtin_fmaf(wk[G * ns + g * ns + k], expf(mk - m), l);
-      }
-      l = wave_sum(l);
-      for (int k = lane; k < ns; k += 64) {
-        const float mk = wk[g * ns + k];
-        wk[g * ns + k] = (m == -INFINITY || mk == -INFINITY || !(l > 0.0f)) ? 0.0f : expf(mk - m) / l;
-      }
-    }
-  }
-  __syncthreads();
-  for (int idx = tid; idx < G * hd; idx += kThreads) {
-    const int g = idx / hd, d = idx % hd;
-    const float* po = p.part_o + (head0 + g) * ns * hd + d;
-    const float* wg = wk + g * ns;
-    float acc = 0.0f;
-    int k = 0;
-    for (; k + 8 <= ns; k += 8) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(po + static_cast<int64_t>(k + u) * hd);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(v[u], wg[k + u], acc);
-    }
-    for (; k < ns; ++k) acc = __builtin_fmaf(__builtin_nontemporal_load(po + static_cast<int64_t>(k) * hd), wg[k], acc);
-    p.out[static_cast<int64_t>(e) * p.ldo + (kvh * G + g) * hd + d] = acc;
-  }
-  if (tid == 0) atomicExch(&p.counters[e * p.hkv + kvh], 0);
 }
 
-size_t attn_smem_bytes(int g, int hd) {
+// Log-sum-exp combine of the splits of one (entry, head): all loads issued up front.
+__global__ __launch_bounds__(kMaxHd) void k_attn_combine(const float* __restrict__ part_o,
+                                                         const float* __restrict__ part_ml, float* __restrict__ out,
+                                                         int64_t ldo, int heads, int hd, int nsplit) {
+  __shared__ float w[kThreads / 2];
+  __shared__ float lsum;
+  const int eh = blockIdx.x;
+  const int e = eh / heads, h = eh % heads;
+  const int t = threadIdx.x;
+  const float* ml = part_ml + static_cast<int64_t>(eh) * nsplit * 2;
+  // nsplit <= 128 = blockDim: thread k owns split k.
+  const float mk = t < nsplit ? ml[2 * t] : -INFINITY;
+  const float lk = t < nsplit ? ml[2 * t + 1] : 0.0f;
+  float m = mk;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  __shared__ float mw[2];
+  if ((t & 63) == 0) mw[t >> 6] = m;
+  __syncthreads();
+  m = fmaxf(mw[0], mw[1]);
+  const float wk = (m == -INFINITY || mk == -INFINITY) ? 0.0f : expf(mk - m);
+  if (t < nsplit) w[t] = wk;
+  float l = lk * wk;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off, 64);
+  __shared__ float lw[2];
+  if ((t & 63) == 0) lw[t >> 6] = l;
+  __syncthreads();
+  if (t == 0) lsum = lw[0] + lw[1];
+  __syncthreads();
+  if (t >= hd) return;
+  const float* po = part_o + static_cast<int64_t>(eh) * nsplit * hd + t;
+  float acc = 0.0f;
+  int k = 0;
+  for (; k + 8 <= nsplit; k += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = po[static_cast<int64_t>(k + u) * hd];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(v[u], w[k + u], acc);
+  }
+  for (; k < nsplit; ++k) acc = __builtin_fmaf(po[static_cast<int64_t>(k) * hd], w[k], acc);
+  out[static_cast<int64_t>(e) * ldo + h * hd + t] = lsum > 0.0f ? acc / lsum : 0.0f;
+}
+
+size_t attn_smem_bytes(int g, int hd, int chunk) {
   const int ngrp = kThreads / (hd / 4);
-  return sizeof(float) * (g * hd + g * kThreads + 2 * g + 2 * hd) + sizeof(int) * (kThreads + 1) +
-         sizeof(float) * ngrp * g * hd;
+  return sizeof(float) * (g * hd + g * chunk + 4 * g + 2 * hd) + sizeof(int) * chunk + sizeof(float) * ngrp * g * hd;
 }
 
 template <int G, int HD, int TPT, bool F>
@@ -357,7 +360,7 @@ void go(const AttnParams& p, dim3 grid, size_t smem, bool fused, hipStream_t st)
 
 template <int G, int HD>
 void by_tpt(const AttnParams& p, dim3 grid, size_t smem, bool fused, hipStream_t st) {
-  const int tpt = kThreads / p.split;
+  const int tpt = kThreads / p.chunk;
   if (tpt == 1) go<G, HD, 1>(p, grid, smem, fused, st);
   else if (tpt == 2) go<G, HD, 2>(p, grid, smem, fused, st);
   else go<G, HD, 4>(p, grid, smem, fused, st);
@@ -374,17 +377,34 @@ void by_hd(const AttnParams& p, dim3 grid, size_t smem, bool fused, hipStream_t 
 }  // namespace
 
 AttnPlan plan_attention(int64_t n, int64_t num_kv_heads, int64_t head_dim, int64_t max_window, int num_cus) {
-  // Widest split (fewest partials) that still gives ~2 workgroups per CU; a split of 64 or
-  // 128 tokens spreads each token over 4 or 2 threads, which needs head_dim % (4 * TPT) == 0.
-  AttnPlan plan{kThreads, 1};
+  // Enough workgroups for ~2 per CU: (entry, kv head) pairs times token splits. Small batches
+  // also shrink the chunk (64 or 128 tokens spread each token over 4 or 2 threads, which needs
+  // head_dim % (4 * TPT) == 0) so that short windows still split. Splits are combined by a
+  // second kernel; at most kThreads / 2 of them.
   const int64_t w = std::max<int64_t>(1, max_window);
-  for (int split : {256, 128, 64}) {
-    const int tpt = kThreads / split;
+  const int64_t pairs = std::max<int64_t>(1, n * num_kv_heads);
+  int64_t want = (2 * static_cast<int64_t>(num_cus) + pairs - 1) / pairs;
+  // PIA_ATTN_MAX_SPLITS caps the split count (the reference's PAGED_INFER_ATTN_LANES_PER_THREAD
+  // plays the same role for its lane schedule, src/attention.rs:46-55).
+  static const int64_t cap = [] {
+    const char* e = std::getenv("PIA_ATTN_MAX_SPLITS");
+    const long v = e ? std::strtol(e, nullptr, 10) : 0;
+    return v > 0 ? static_cast<int64_t>(v) : int64_t(0);
+  }();
+  if (cap) want = std::min(want, cap);
+  AttnPlan plan{w, 1, kThreads};
+  for (int chunk : {256, 128, 64}) {
+    const int tpt = kThreads / chunk;
     if (head_dim % (4 * tpt) != 0) break;
-    plan.split = split;
-    plan.splits = (w + split - 1) / split;
-    if (n * num_kv_heads * plan.splits >= 2 * static_cast<int64_t>(num_cus)) break;
+    plan.chunk = chunk;
+    plan.splits = std::min<int64_t>(std::min<int64_t>((w + chunk - 1) / chunk, want), kThreads / 2);
+    if (plan.splits >= want) break;
   }
+  plan.splits = std::max<int64_t>(1, plan.splits);
+  int64_t split = (w + plan.splits - 1) / plan.splits;
+  split = (split + plan.chunk - 1) / plan.chunk * plan.chunk;
+  plan.split = split;
+  plan.splits = (w + split - 1) / split;
   return plan;
 }
 
@@ -400,11 +420,11 @@ void launch_attention(const AttnLaunch& a, hipStream_t st) {
   PIA_REQUIRE(L.head_dim % 4 == 0 && L.head_dim <= kMaxHd, "attention: head_dim must be a multiple of 4 and <= 128");
   PIA_REQUIRE(a.layer >= 0 && a.layer < L.num_layers, "attention: layer out of range");
   PIA_REQUIRE(L.num_blocks * L.block_size < (int64_t(1) << 31), "attention: too many cache slots for int32 indexing");
-  PIA_REQUIRE(a.plan.splits >= 1 && a.plan.splits <= kThreads / 2,
-              "attention: at most 128 token splits (windows up to 32768 tokens)");
-  PIA_REQUIRE(a.plan.split == 64 || a.plan.split == 128 || a.plan.split == 256, "attention: bad split size");
-  PIA_REQUIRE(L.head_dim % (4 * (kThreads / a.plan.split)) == 0, "attention: split size does not fit head_dim");
-  PIA_REQUIRE(a.plan.splits == 1 || (a.work && a.counters), "attention: split-K needs a workspace and counters");
+  PIA_REQUIRE(a.plan.splits >= 1 && a.plan.splits <= kThreads / 2, "attention: at most 128 token splits");
+  PIA_REQUIRE(a.plan.chunk == 64 || a.plan.chunk == 128 || a.plan.chunk == 256, "attention: bad chunk size");
+  PIA_REQUIRE(a.plan.split >= 1 && a.plan.split % a.plan.chunk == 0, "attention: split must be whole chunks");
+  PIA_REQUIRE(L.head_dim % (4 * (kThreads / a.plan.chunk)) == 0, "attention: chunk size does not fit head_dim");
+  PIA_REQUIRE(a.plan.splits == 1 || a.work, "attention: split windows need a workspace");
   PIA_REQUIRE(!a.fused || (a.rope_cos && a.rope_sin), "attention: fused RoPE needs the rotary tables");
   if (a.n == 0) return;
   const int g = static_cast<int>(a.heads / L.num_kv_heads);
@@ -424,14 +444,14 @@ void launch_attention(const AttnLaunch& a, hipStream_t st) {
   p.entries = a.entries;
   p.tables = a.tables;
   p.split = static_cast<int>(a.plan.split);
+  p.chunk = static_cast<int>(a.plan.chunk);
   p.nsplit = static_cast<int>(a.plan.splits);
   p.part_o = static_cast<float*>(a.work);
   p.part_ml = p.part_o ? p.part_o + a.n * a.heads * a.plan.splits * hd : nullptr;
-  p.counters = a.counters;
   p.rope_cos = a.rope_cos;
   p.rope_sin = a.rope_sin;
   dim3 grid(static_cast<unsigned>(a.plan.splits), static_cast<unsigned>(L.num_kv_heads), static_cast<unsigned>(a.n));
-  const size_t smem = attn_smem_bytes(g, hd);
+  const size_t smem = attn_smem_bytes(g, hd, static_cast<int>(a.plan.chunk));
   switch (g) {
     case 1: by_hd<1>(p, grid, smem, a.fused, st); break;
     case 2: by_hd<2>(p, grid, smem, a.fused, st); break;
@@ -441,6 +461,11 @@ void launch_attention(const AttnLaunch& a, hipStream_t st) {
     default: fail(PIA_ERR_INVALID, "attention: kv_group must be 1, 2, 4, 8 or 16");
   }
   PIA_HIP(hipGetLastError());
+  if (a.plan.splits > 1) {
+    hipLaunchKernelGGL(k_attn_combine, dim3(static_cast<unsigned>(a.n * a.heads)), dim3(kMaxHd), 0, st, p.part_o,
+                       p.part_ml, a.out, a.ldo, static_cast<int>(a.heads), hd, static_cast<int>(a.plan.splits));
+    PIA_HIP(hipGetLastError());
+  }
 }
 
 }  // namespace pia

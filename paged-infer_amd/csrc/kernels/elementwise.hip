@@ -31,7 +31,7 @@ __global__ __launch_bounds__(kThreads) void k_embed(const int32_t* __restrict__ 
                                                     float* __restrict__ x, int64_t ldx, int64_t hidden, int64_t vocab,
                                                     unsigned long long* __restrict__ amax) {
   const int b = blockIdx.x;
-  if (amax && threadIdx.x == 0) amax[b] = 0ull;
+  if (amax && threadIdx.x < kArgmaxSlots) amax[b * kArgmaxSlots + threadIdx.x] = 0ull;
   const int64_t tok = static_cast<int64_t>(static_cast<uint32_t>(tokens[b])) % vocab;
   const uint16_t* src = emb + tok * hidden;
   float* dst = x + static_cast<int64_t>(b) * ldx;
@@ -45,11 +45,24 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm(const float* __restrict__ 
   __shared__ float red[kThreads / 64 + 1];
   const float* xr = x + static_cast<int64_t>(blockIdx.x) * ldx;
   float* orow = out + static_cast<int64_t>(blockIdx.x) * ldo;
+  constexpr int kPer = 16;  // rows up to 4096 stay in registers; longer rows take a second pass
+  float v[kPer];
   float ss = 0.0f;
-  for (int i = threadIdx.x; i < n; i += kThreads) ss += xr[i] * xr[i];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int i = threadIdx.x + u * kThreads;
+    v[u] = i < n ? xr[i] : 0.0f;
+    ss += v[u] * v[u];
+  }
+  for (int i = threadIdx.x + kPer * kThreads; i < n; i += kThreads) ss += xr[i] * xr[i];
   ss = block_sum(ss, red);
   const float inv = 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
-  for (int i = threadIdx.x; i < n; i += kThreads) orow[i] = (xr[i] * inv) * w[i];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int i = threadIdx.x + u * kThreads;
+    if (i < n) orow[i] = (v[u] * inv) * w[i];
+  }
+  for (int i = threadIdx.x + kPer * kThreads; i < n; i += kThreads) orow[i] = (xr[i] * inv) * w[i];
 }
 
 // src/model.rs:1068-1107: rotate every q head and (once) every kv head, then write K and V

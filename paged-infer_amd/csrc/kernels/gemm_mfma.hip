@@ -1,0 +1,320 @@
+// Batched int8 projection on the matrix cores (decode batches >= 8 and prefill).
+//
+// The reference multiplies int8 weights by f32 activations in f32 (src/math.rs:223-275). On
+// gfx950 the int8 matrix core (v_mfma_i32_16x16x64_i8) is 2x the bf16 rate and consumes the
+// stored weights as they are, with no widening. To feed it f32 activations without losing
+// f32-level accuracy, each activation row x_b is written in 23-bit fixed point relative to its
+// own power-of-two range, v = rint(x * 2^(22 - e_b)) with max|x_b| < 2^e_b, and v is split
+// into three signed base-256 digits, v = d0 + 256 d1 + 65536 d2. Each digit is an int8
+// column of the B operand, so one MFMA pass computes sum_k W[r][k] * d_j[b][k] for all three
+// digits exactly in int32. The epilogue recombines y = (C0 + 256 C1 + 65536 C2) * 2^(e_b-22)
+// * scale[r]. The only rounding is the fixed-point image of x (|error| <= 2^-23 max|x_b| per
+// element) and the final conversion -- tighter than an f32 accumulation of the same dot.
+#include <cmath>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace pia {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+
+__device__ inline float block_reduce_sum(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) t += red[w];
+  return t;
+}
+__device__ inline float block_reduce_max(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) t = fmaxf(t, red[w]);
+  return t;
+}
+
+// One workgroup per activation row b (rows >= batch write zero digits). Optional RMSNorm.
+__global__ __launch_bounds__(kThreads) void k_xdigits(const float* __restrict__ x, int64_t ldx,
+                                                      const float* __restrict__ nw, float eps, int cols, int batch,
+                                                      int kpad, int8_t* __restrict__ dig, float* __restrict__ pow2) {
+  __shared__ float red[kThreads / 64];
+  const int b = blockIdx.x;
+  int8_t* d0 = dig + static_cast<int64_t>(3 * b) * kpad;
+  int8_t* d1 = d0 + kpad;
+  int8_t* d2 = d1 + kpad;
+  if (b >= batch) {
+    for (int k = threadIdx.x; k < kpad; k += kThreads) d0[k] = d1[k] = d2[k] = 0;
+    if (threadIdx.x == 0) pow2[b] = 0.0f;
+    return;
+  }
+  const float* xr = x + static_cast<int64_t>(b) * ldx;
+  // The row is held in registers: kPer values per thread, loaded together (cols <= kThreads *
+  // kPer; longer rows take the strided path).
+  constexpr int kPer = 64;
+  float xv[kPer];
+  const bool in_regs = cols <= kThreads * kPer;
+  float inv = 1.0f;
+  if (in_regs) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int k = threadIdx.x + u * kThreads;
+      xv[u] = k < cols ? xr[k] : 0.0f;
+    }
+    if (nw) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) ss += xv[u] * xv[u];
+      ss = block_reduce_sum(ss, red);
+      inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int k = threadIdx.x + u * kThreads;
+        xv[u] = k < cols ? (xv[u] * inv) * nw[k] : 0.0f;
+      }
+    }
+  } else if (nw) {
+    float ss = 0.0f;
+    for (int k = threadIdx.x; k < cols; k += kThreads) ss += xr[k] * xr[k];
+    ss = block_reduce_sum(ss, red);
+    inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+  }
+  float m = 0.0f;
+  if (in_regs) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) m = fmaxf(m, fabsf(xv[u]));
+  } else {
+    for (int k = threadIdx.x; k < cols; k += kThreads) m = fmaxf(m, fabsf(nw ? (xr[k] * inv) * nw[k] : xr[k]));
+  }
+  m = block_reduce_max(m, red);
+  int e = 0;
+  if (m > 0.0f) (void)frexpf(m, &e);  // m = f * 2^e, f in [0.5, 1): max|x| < 2^e
+  const int sh = 22 - e;
+  auto put = [&](int k, float v_in) {
+    const int v = static_cast<int>(rintf(ldexpf(v_in, sh)));  // |v| <= 2^22
+    const int a0 = ((v + 128) & 255) - 128;
+    const int v1 = (v - a0) >> 8;
+    const int a1 = ((v1 + 128) & 255) - 128;
+    const int a2 = (v1 - a1) >> 8;  // |a2| <= 64
+    d0[k] = static_cast<int8_t>(a0);
+    d1[k] = static_cast<int8_t>(a1);
+    d2[k] = static_cast<int8_t>(a2);
+  };
+  if (in_regs) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int k = threadIdx.x + u * kThreads;
+      if (k < kpad) put(k, xv[u]);  // zero beyond cols: kpad <= cols + 63 <= kThreads * kPer + 63
+    }
+    for (int k = kThreads * kPer + threadIdx.x; k < kpad; k += kThreads) put(k, 0.0f);
+  } else {
+    for (int k = threadIdx.x; k < kpad; k += kThreads) put(k, k < cols ? (nw ? (xr[k] * inv) * nw[k] : xr[k]) : 0.0f);
+  }
+  if (threadIdx.x == 0) pow2[b] = ldexpf(1.0f, -sh);
+}
+
+enum { kEpiStore = 0, kEpiAdd = 1, kEpiSwiglu = 2 };
+
+__device__ inline uint32_t order_key(float f) {
+  const uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Decode GEMM: one workgroup per 16 weight rows x NT*16 digit columns (all of the batch's
+// digits for NT <= 12); the 4 wavefronts split K (interleaved 64-wide steps) and their int32
+// partial sums are added in LDS. Every weight byte is read once per launch.
+template <int NT, int EPI, bool AMAX>
+__global__ __launch_bounds__(kThreads) void k_gemm_dec(const int8_t* __restrict__ W, int64_t ldw,
+                                                       const float* __restrict__ S, const int8_t* __restrict__ D,
+                                                       int kpad, const float* __restrict__ pow2,
+                                                       float* __restrict__ O, int64_t osb, int64_t osr, int rows,
+                                                       int batch, unsigned long long* __restrict__ amax) {
+  __shared__ int csum[4][16][NT * 16];
+  __shared__ unsigned long long best[AMAX ? 64 : 1];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = blockIdx.x * 16;
+  if (AMAX && threadIdx.x < 64) best[threadIdx.x] = 0ull;
+  // grid.y: chunk of `batch` entries (64 per chunk when there are several).
+  D += static_cast<int64_t>(blockIdx.y) * 3 * batch * kpad;
+  O += static_cast<int64_t>(blockIdx.y) * batch * osb;
+  pow2 += static_cast<int64_t>(blockIdx.y) * batch;
+  if (AMAX) amax += static_cast<int64_t>(blockIdx.y) * batch * kArgmaxSlots;
+  const int r_l = lane & 15, kg = lane >> 4;  // operand row / column within the tile, k group
+  const int8_t* wp = W + static_cast<int64_t>(min(row0 + r_l, rows - 1)) * ldw + kg * 16;
+  const int8_t* dp = D + static_cast<int64_t>(r_l) * kpad + kg * 16;
+  v4i acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = v4i{0, 0, 0, 0};
+  const int ksteps = kpad / 64;
+  constexpr int kU = 4;  // k-steps per wave whose loads are in flight together
+  for (int s0 = wave; s0 < ksteps; s0 += 4 * kU) {
+    v4i a[kU];
+    v4i bm[kU][NT];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int s = s0 + 4 * u;
+      if (s < ksteps) {
+        a[u] = *reinterpret_cast<const v4i*>(wp + s * 64);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          bm[u][t] = *reinterpret_cast<const v4i*>(dp + static_cast<int64_t>(t * 16) * kpad + s * 64);
+      } else {
+        a[u] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < NT; ++t) bm[u][t] = v4i{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], bm[u][t], acc[t], 0, 0, 0);
+  }
+  // 16x16 int32 result tile t: lane holds rows 4*(lane/16) + v, column lane % 16.
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) csum[wave][4 * kg + v][t * 16 + r_l] = acc[t][v];
+  __syncthreads();
+
+  // Epilogue: thread -> (row, batch entry); the three digit columns of b are 3b, 3b+1, 3b+2.
+  for (int idx = threadIdx.x; idx < 16 * batch; idx += kThreads) {
+    const int r = idx / batch, b = idx % batch;
+    const int row = row0 + r;
+    int64_t c[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int col = 3 * b + j;
+      c[j] = static_cast<int64_t>(csum[0][r][col]) + csum[1][r][col] + csum[2][r][col] + csum[3][r][col];
+    }
+    const int64_t sum = c[0] + 256 * c[1] + 65536 * c[2];
+    const float y = static_cast<float>(sum) * pow2[b];
+    if constexpr (EPI == kEpiSwiglu) {
+      if ((r & 1) == 0 && row + 1 < rows) {
+        int64_t cu[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          const int col = 3 * b + j;
+          cu[j] = static_cast<int64_t>(csum[0][r + 1][col]) + csum[1][r + 1][col] + csum[2][r + 1][col] +
+                  csum[3][r + 1][col];
+        }
+        const float yu = static_cast<float>(cu[0] + 256 * cu[1] + 65536 * cu[2]) * pow2[b];
+        const float g = y * S[row];
+        const float u = yu * S[row + 1];
+        const float silu = g / (1.0f + expf(-g));
+        O[static_cast<int64_t>(b) * osb + static_cast<int64_t>(row >> 1) * osr] = silu * u;
+      }
+    } else if (row < rows) {
+      const float v = y * S[row];
+      float* o = O + static_cast<int64_t>(b) * osb + static_cast<int64_t>(row) * osr;
+      if (EPI == kEpiAdd) *o = *o + v;
+      else *o = v;
+      if constexpr (AMAX) {
+        const unsigned long long cand = (static_cast<unsigned long long>(order_key(v)) << 32) | static_cast<uint32_t>(row);
+        atomicMax(&best[b], cand);  // LDS: the 16 rows of this tile first
+      }
+    }
+  }
+  if constexpr (AMAX) {
+    __syncthreads();
+    // Then one atomic per batch entry and workgroup, spread over the slots.
+    if (threadIdx.x < batch)
+      atomicMax(&amax[threadIdx.x * kArgmaxSlots + (blockIdx.x & (kArgmaxSlots - 1))], best[threadIdx.x]);
+  }
+}
+
+template <int NT>
+void go_dec(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, const float* pow2, float* O,
+            int64_t osb, int64_t osr, int rows, int batch, int chunks, Epi epi, unsigned long long* amax,
+            hipStream_t st) {
+  dim3 grid((rows + 15) / 16, chunks);
+  if (epi == Epi::Add)
+    hipLaunchKernelGGL((k_gemm_dec<NT, kEpiAdd, false>), grid, dim3(kThreads), 0, st, W, ldw, S, D, kpad, pow2, O, osb,
+                       osr, rows, batch, amax);
+  else if (epi == Epi::Swiglu)
+    hipLaunchKernelGGL((k_gemm_dec<NT, kEpiSwiglu, false>), grid, dim3(kThreads), 0, st, W, ldw, S, D, kpad, pow2, O,
+                       osb, osr, rows, batch, amax);
+  else if (amax)
+    hipLaunchKernelGGL((k_gemm_dec<NT, kEpiStore, true>), grid, dim3(kThreads), 0, st, W, ldw, S, D, kpad, pow2, O,
+                       osb, osr, rows, batch, amax);
+  else
+    hipLaunchKernelGGL((k_gemm_dec<NT, kEpiStore, false>), grid, dim3(kThreads), 0, st, W, ldw, S, D, kpad, pow2, O,
+                       osb, osr, rows, batch, amax);
+}
+
+}  // namespace
+
+int64_t digit_cols(int64_t batch) { return (3 * batch + 15) / 16 * 16; }
+
+// Digit rows written by k_xdigits: whole triples covering digit_cols(batch) columns.
+int64_t digit_rows(int64_t batch) { return (digit_cols(batch) + 2) / 3 * 3; }
+
+int64_t xdigits_bytes(int64_t batch, int64_t cols) {
+  const int64_t kpad = (cols + 63) / 64 * 64;
+  return (digit_rows(batch) * kpad + 255) / 256 * 256 + digit_rows(batch) / 3 * 4;
+}
+
+void launch_xdigits(const float* x, int64_t ldx, const float* norm_w, float eps, int64_t batch, int64_t cols,
+                    void* xq, hipStream_t st) {
+  PIA_REQUIRE(batch > 0 && cols > 0 && cols < (int64_t(1) << 30), "xdigits: bad shape");
+  const int64_t kpad = (cols + 63) / 64 * 64;
+  const int64_t n = digit_rows(batch);
+  int8_t* dig = static_cast<int8_t*>(xq);
+  float* pow2 = reinterpret_cast<float*>(dig + (n * kpad + 255) / 256 * 256);
+  const int64_t groups = n / 3;  // digit-column triples (batch rows, padded with zeros)
+  hipLaunchKernelGGL(k_xdigits, dim3(static_cast<unsigned>(groups)), dim3(kThreads), 0, st, x, ldx, norm_w, eps,
+                     static_cast<int>(cols), static_cast<int>(batch), static_cast<int>(kpad), dig, pow2);
+  PIA_HIP(hipGetLastError());
+}
+
+void launch_gemm_i8_mfma(const int8_t* W, int64_t ldw, const float* scales, const void* xq, float* out, int64_t osb,
+                         int64_t osr, int64_t rows, int64_t cols, int64_t batch, Epi epi, unsigned long long* amax,
+                         hipStream_t st) {
+  const int64_t kpad = (cols + 63) / 64 * 64;
+  PIA_REQUIRE(ldw >= kpad && ldw % 16 == 0, "gemm: weight rows must be padded to a multiple of 64 bytes");
+  PIA_REQUIRE(scales != nullptr, "gemm: int8 weights need scales");
+  PIA_REQUIRE(rows > 0 && rows < (int64_t(1) << 31), "gemm: bad row count");
+  PIA_REQUIRE(epi != Epi::Swiglu || rows % 2 == 0, "gemm: SwiGLU needs interleaved row pairs");
+  PIA_REQUIRE(!amax || epi == Epi::Store, "gemm: fused argmax needs the Store epilogue");
+  const int8_t* dig = static_cast<const int8_t*>(xq);
+  const int64_t n = digit_rows(batch);
+  const float* pow2 = reinterpret_cast<const float*>(dig + (n * kpad + 255) / 256 * 256);
+  const int r = static_cast<int>(rows), k = static_cast<int>(kpad);
+  // Column tiles of 64 batch entries (12 x 16 digit columns) along grid.y, then the ragged
+  // remainder as its own launch.
+  const int64_t full = batch / 64;
+  auto launch = [&](int64_t b0, int64_t chunks, int nb) {
+    const int nt = static_cast<int>(digit_cols(nb) / 16);
+    const int8_t* D = dig + 3 * b0 * kpad;
+    float* O = out + b0 * osb;
+    unsigned long long* am = amax ? amax + b0 * kArgmaxSlots : nullptr;
+    const float* p2 = pow2 + b0;
+    switch (nt) {
+#define PIA_NT(N)                                                                                     \
+  case N:                                                                                             \
+    go_dec<N>(W, ldw, scales, D, k, p2, O, osb, osr, r, nb, static_cast<int>(chunks), epi, am, st); \
+    break;
+      PIA_NT(1) PIA_NT(2) PIA_NT(3) PIA_NT(4) PIA_NT(5) PIA_NT(6) PIA_NT(7) PIA_NT(8) PIA_NT(9) PIA_NT(10)
+      PIA_NT(11) PIA_NT(12)
+#undef PIA_NT
+      default: fail(PIA_ERR_INVALID, "gemm: bad column tile");
+    }
+  };
+  if (full) launch(0, full, 64);
+  if (batch % 64) launch(full * 64, 1, static_cast<int>(batch % 64));
+  PIA_HIP(hipGetLastError());
+}
+
+}  // namespace pia

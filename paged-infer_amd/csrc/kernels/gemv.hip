@@ -139,11 +139,27 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv(const TW* __restrict__ W, 
   load_batch(0);  // in flight while the RMSNorm prologue runs
 
   if constexpr (NORM) {
-    // 1/rms of each batch row (src/math.rs:12-18), computed by the whole workgroup.
+    // 1/rms of each batch row (src/math.rs:12-18), computed by the whole workgroup; the row is
+    // read with 16-byte loads, all in flight together (cols % 4 == 0 on this path).
     for (int b = 0; b < batch; ++b) {
       const float* xr = X + static_cast<int64_t>(b) * ldx;
       float ss = 0.0f;
-      for (int i = threadIdx.x; i < cols; i += 64 * kWaves) ss += xr[i] * xr[i];
+      if (cols % 4 == 0 && (reinterpret_cast<uintptr_t>(xr) & 15) == 0) {
+        const float4* x4 = reinterpret_cast<const float4*>(xr);
+        const int n4 = cols / 4;
+        for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * 64 * kWaves) {
+          float4 v[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int i = i0 + u * 64 * kWaves;
+            v[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
+        }
+      } else {
+        for (int i = threadIdx.x; i < cols; i += 64 * kWaves) ss += xr[i] * xr[i];
+      }
       ss = wave_sum(ss);
       if (lane == 0) red[wave] = ss;
       __syncthreads();
@@ -245,11 +261,8 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv(const TW* __restrict__ W, 
           if (valid && b_l == b)
             cand = (static_cast<unsigned long long>(order_key(v)) << 32) | static_cast<uint32_t>(row);
           cand = wave_max_u64(cand);
-          // Most waves lose to the running maximum: test before taking the atomic, so only a
-          // few of the thousands of waves contend on the slot.
-          if (lane == 0 && b0 + b < batch &&
-              cand > __hip_atomic_load(&amax[b0 + b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-            atomicMax(&amax[b0 + b], cand);
+          if (lane == 0 && b0 + b < batch)
+            atomicMax(&amax[(b0 + b) * kArgmaxSlots + ((blockIdx.x * kWaves + wave) & (kArgmaxSlots - 1))], cand);
         }
       }
     }

@@ -113,8 +113,8 @@ _SIGS = {
     "pia_model_decode": (I32, [P, P, P, P, P, P, I64, P, P]),
     "pia_model_prefill": (I32, [P, P, I64, I64, P, I64, P, P]),
     "pia_model_profile": (I32, [P, I32]),
-    "pia_model_profile_get": (I32, [P, P, P, I32]),
-    "pia_bench_projection": (I32, [P, I64, I64, I64, I32, C.POINTER(C.c_double), C.POINTER(I64)]),
+    "pia_model_profile_get": (I32, [P, P, P, P, I32]),
+    "pia_bench_projection": (I32, [P, I64, I64, I64, I32, I32, C.POINTER(C.c_double), C.POINTER(I64)]),
     "pia_synth_normal": (I32, [U64, U64, F32, P, I64]),
     "pia_f32_to_bf16": (I32, [P, P, I64]),
 }
@@ -254,10 +254,13 @@ class DeviceArray:
             pass
 
 
-def bench_projection(ctx: "Context", rows: int, cols: int, batch: int = 1, reps: int = 20):
+BENCH_NORM, BENCH_SWIGLU, BENCH_ADD, BENCH_MFMA = 1, 2, 4, 8
+
+
+def bench_projection(ctx: "Context", rows: int, cols: int, batch: int = 1, reps: int = 20, flags: int = 0):
     """(microseconds per launch, algorithmic bytes per launch) of one int8 projection shape."""
     us, by = C.c_double(), I64()
-    check(lib().pia_bench_projection(ctx.h, rows, cols, batch, reps, C.byref(us), C.byref(by)))
+    check(lib().pia_bench_projection(ctx.h, rows, cols, batch, reps, flags, C.byref(us), C.byref(by)))
     return us.value, by.value
 
 
@@ -486,11 +489,16 @@ class Model:
     def profile(self, on: bool):
         check(lib().pia_model_profile(self.h, int(on)))
 
+    PROFILE_CLASSES = ("qkv", "o", "gate_up", "down", "lm_head", "attention", "other")
+
     def profile_get(self):
-        ms = np.zeros(3, np.float64)
-        by = np.zeros(3, np.int64)
-        check(lib().pia_model_profile_get(self.h, ptr(ms), ptr(by), 3))
-        return ms, by
+        """(ms, algorithmic bytes, launches) per class of the last profiled call."""
+        n = len(self.PROFILE_CLASSES)
+        ms = np.zeros(n, np.float64)
+        by = np.zeros(n, np.int64)
+        calls = np.zeros(n, np.int64)
+        check(lib().pia_model_profile_get(self.h, ptr(ms), ptr(by), ptr(calls), n))
+        return ms, by, calls
 
 
 # ------------------------------------------------------------------------------------------
