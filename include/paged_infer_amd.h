@@ -233,6 +233,12 @@ pia_status pia_model_prefill(pia_model* m, const uint32_t* tokens, int64_t n, in
 pia_status pia_model_profile(pia_model* m, int32_t enable);
 pia_status pia_model_profile_get(pia_model* m, double* ms_per_class, int64_t* bytes_per_class,
                                  int64_t* calls_per_class, int32_t n_class);
+/* Mean device time of one launch of a projection class (0..4 above) at `batch`, from a graph
+ * of that class's launches over every layer (the model's weights, buffers and kernels of a
+ * decode step), and the algorithmic bytes of one launch. Overwrites the activation buffers.
+ * No counterpart in the reference. */
+pia_status pia_model_bench_class(pia_model* m, int32_t cls, int64_t batch, int32_t reps, double* us,
+                                 int64_t* bytes);
 
 /* ------------------------------------------------------------------------------------ */
 /* Diagnostics (no counterpart in the reference).                                         */

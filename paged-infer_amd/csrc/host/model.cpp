@@ -539,6 +539,78 @@ pia_status pia_model_profile_get(pia_model* m, double* ms, int64_t* bytes, int64
   PIA_API_END
 }
 
+// Device time per launch of one projection class (0 = q/k/v, 1 = o, 2 = gate/up, 3 = down,
+// 4 = LM head) at `batch`: the class's launches for every layer (the model's own weights and
+// buffers, the exact kernels and arguments of a decode step) captured `reps` times in one graph,
+// HIP events around a replay. Inter-kernel gaps inside a graph are ~0.25 us on MI355X.
+pia_status pia_model_bench_class(pia_model* m, int32_t cls, int64_t batch, int32_t reps, double* us,
+                                 int64_t* bytes) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(m && us && bytes, "null argument");
+  PIA_REQUIRE(cls >= 0 && cls <= 4 && batch > 0 && batch <= kFusedNormRows && reps > 0 && reps <= 100,
+              "bad profiling request");
+  m->check_complete();
+  PIA_HIP(hipSetDevice(m->ctx->device));
+  m->ensure_cap(batch);
+  m->grow(m->logits, batch * m->ld_v * 4);
+  const bool prof_was = m->prof.on;
+  m->prof.on = false;
+  hipStream_t st = m->st();
+  float* X = m->x.as<float>();
+  float* H = m->h.as<float>();
+  auto launch = [&](int64_t l) {
+    Layer& L = m->layers[l];
+    switch (cls) {
+      case 0: m->normed_gemv(L.qkv, X, L.attn_norm.as<float>(), batch, m->qkv.as<float>(), m->ld_qkv, Epi::Store); break;
+      case 1: m->gemv(L.o, m->attn.as<float>(), m->ld_h, nullptr, X, m->ld_h, batch, Epi::Add); break;
+      case 2: m->normed_gemv(L.gu, X, L.ffn_norm.as<float>(), batch, H, m->ld_i, Epi::Swiglu); break;
+      case 3: m->gemv(L.down, H, m->ld_i, nullptr, X, m->ld_h, batch, Epi::Add); break;
+      default:
+        m->normed_gemv(m->lm_head, X, m->final_norm.as<float>(), batch, m->logits.as<float>(), m->ld_v, Epi::Store,
+                       m->amax.as<unsigned long long>());
+    }
+  };
+  const int64_t per = cls == 4 ? 1 : m->cfg.layers;
+  const Proj& probe = cls == 4 ? m->lm_head : cls == 0 ? m->layers[0].qkv : cls == 1 ? m->layers[0].o
+                      : cls == 2 ? m->layers[0].gu : m->layers[0].down;
+  PIA_HIP(hipMemsetAsync(X, 0, batch * m->ld_h * 4, st));  // finite inputs for the timed launches
+  PIA_HIP(hipMemsetAsync(H, 0, batch * m->ld_i * 4, st));
+  PIA_HIP(hipMemsetAsync(m->attn.ptr, 0, batch * m->ld_h * 4, st));
+  for (int64_t l = 0; l < per; ++l) launch(l);  // warm: also fills the digit workspace
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  PIA_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
+  try {
+    for (int r = 0; r < reps; ++r)
+      for (int64_t l = 0; l < per; ++l) launch(l);
+  } catch (...) {
+    (void)hipStreamEndCapture(st, &graph);
+    if (graph) (void)hipGraphDestroy(graph);
+    m->prof.on = prof_was;
+    throw;
+  }
+  PIA_HIP(hipStreamEndCapture(st, &graph));
+  PIA_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+  hipEvent_t e0, e1;
+  PIA_HIP(hipEventCreate(&e0));
+  PIA_HIP(hipEventCreate(&e1));
+  PIA_HIP(hipGraphLaunch(exec, st));
+  PIA_HIP(hipEventRecord(e0, st));
+  PIA_HIP(hipGraphLaunch(exec, st));
+  PIA_HIP(hipEventRecord(e1, st));
+  PIA_HIP(hipStreamSynchronize(st));
+  float ms = 0;
+  PIA_HIP(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  (void)hipGraphExecDestroy(exec);
+  (void)hipGraphDestroy(graph);
+  m->prof.on = prof_was;
+  *us = 1e3 * ms / static_cast<double>(reps * per);
+  *bytes = pia_model::proj_bytes(probe, batch, cls == 2 ? Epi::Swiglu : Epi::Store);
+  PIA_API_END
+}
+
 }  // extern "C"
 
 namespace {

@@ -221,19 +221,22 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnParams p) {
     }
     __syncthreads();
 
-    // V accumulation: hd/4 threads per token group, 4 consecutive dims each; 4 tokens' loads
-    // in flight per thread.
+    // V accumulation: hd/4 threads per token group, 4 consecutive dims each. With a
+    // compile-time head_dim every token of the chunk a thread owns is loaded before the first
+    // FMA (kChunk / ngrp loads in flight); otherwise 4 at a time.
     if (grp < ngrp) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const float alpha = stat[4 * g + 2];
         o[g][0] *= alpha, o[g][1] *= alpha, o[g][2] *= alpha, o[g][3] *= alpha;
       }
-      for (int i0 = grp; i0 < count; i0 += 4 * ngrp) {
-        float4 v4[4];
-        int idx[4];
+      constexpr int kVTfull = HD ? kChunk / (kThreads / (HD ? HD / 4 : 1)) : 4;
+      constexpr int kVT = kVTfull < 16 ? kVTfull : 16;  // tokens per thread per pass
+      for (int i0 = grp; i0 < count; i0 += kVT * ngrp) {
+        float4 v4[kVT];
+        int idx[kVT];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kVT; ++u) {
           const int i = i0 + u * ngrp;
           const int slot = i < count ? slot_of[i] : -1;
           idx[u] = slot >= 0 ? i : -1;
@@ -245,7 +248,7 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnParams p) {
           }
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kVT; ++u) {
           if (idx[u] < 0) continue;
 #pragma unroll
           for (int g = 0; g < G; ++g) {
@@ -383,7 +386,13 @@ AttnPlan plan_attention(int64_t n, int64_t num_kv_heads, int64_t head_dim, int64
   // second kernel; at most kThreads / 2 of them.
   const int64_t w = std::max<int64_t>(1, max_window);
   const int64_t pairs = std::max<int64_t>(1, n * num_kv_heads);
-  int64_t want = (2 * static_cast<int64_t>(num_cus) + pairs - 1) / pairs;
+  // PIA_ATTN_WGS_PER_CU sets the workgroups-per-CU target of the split (default 2).
+  static const int64_t per_cu = [] {
+    const char* e = std::getenv("PIA_ATTN_WGS_PER_CU");
+    const long v = e ? std::strtol(e, nullptr, 10) : 0;
+    return v > 0 ? static_cast<int64_t>(v) : int64_t(2);
+  }();
+  int64_t want = (per_cu * static_cast<int64_t>(num_cus) + pairs - 1) / pairs;
   // PIA_ATTN_MAX_SPLITS caps the split count (the reference's PAGED_INFER_ATTN_LANES_PER_THREAD
   // plays the same role for its lane schedule, src/attention.rs:46-55).
   static const int64_t cap = [] {

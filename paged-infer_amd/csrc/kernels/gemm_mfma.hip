@@ -235,10 +235,174 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dec(const int8_t* __restrict_
   }
 }
 
+// Tall-matrix decode GEMM: one workgroup per 64 weight rows (wave w owns rows 16w..16w+15 over
+// the full K) x NT*16 digit columns. The digit operand is staged once per workgroup in LDS, in
+// double-buffered KC-byte K chunks (row pitch padded by 16 bytes against bank conflicts). The
+// next chunk's weights and digits are loaded into registers before the current chunk's MFMAs
+// and written to LDS after them, so one memory round trip overlaps one chunk of compute.
+template <int NT>
+struct Rows64 {
+  static constexpr int kN = NT * 16;
+  static constexpr int kKC = NT <= 6 ? 512 : 256;          // bytes of K per stage
+  static constexpr int kPitch = kKC + 16;                  // LDS row pitch
+  static constexpr int kDig = kN * (kKC / 16) / kThreads;  // 16-byte digit loads per thread
+  static_assert(kN * (kKC / 16) % kThreads == 0, "digit tile must split evenly");
+};
+
+template <int NT, int EPI, bool AMAX>
+__global__ __launch_bounds__(kThreads) void k_gemm_rows64(const int8_t* __restrict__ W, int64_t ldw,
+                                                          const float* __restrict__ S, const int8_t* __restrict__ D,
+                                                          int kpad, const float* __restrict__ pow2,
+                                                          float* __restrict__ O, int64_t osb, int64_t osr, int rows,
+                                                          int batch, unsigned long long* __restrict__ amax) {
+  using T = Rows64<NT>;
+  constexpr int kN = T::kN, kKC = T::kKC, kPitch = T::kPitch, kDig = T::kDig, kU = kKC / 64;
+  extern __shared__ int8_t lds[];  // [2][kN][kPitch] digits; reused as int32 C [64][kN]
+  __shared__ unsigned long long best[AMAX ? 64 : 1];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = blockIdx.x * 64;
+  D += static_cast<int64_t>(blockIdx.y) * 3 * batch * kpad;
+  O += static_cast<int64_t>(blockIdx.y) * batch * osb;
+  pow2 += static_cast<int64_t>(blockIdx.y) * batch;
+  if (AMAX) amax += static_cast<int64_t>(blockIdx.y) * batch * kArgmaxSlots;
+  if (AMAX && threadIdx.x < 64) best[threadIdx.x] = 0ull;
+  const int r_l = lane & 15, kg = lane >> 4;
+  const int8_t* wp = W + static_cast<int64_t>(min(row0 + wave * 16 + r_l, rows - 1)) * ldw + kg * 16;
+  const int nchunks = (kpad + kKC - 1) / kKC;
+
+  auto load_d = [&](int c, v4i (&d)[kDig]) {
+#pragma unroll
+    for (int i = 0; i < kDig; ++i) {
+      const int idx = threadIdx.x + i * kThreads;
+      const int n = idx / (kKC / 16), j = (idx % (kKC / 16)) * 16;
+      const int k = c * kKC + j;
+      d[i] = k < kpad ? *reinterpret_cast<const v4i*>(D + static_cast<int64_t>(n) * kpad + k) : v4i{0, 0, 0, 0};
+    }
+  };
+  auto store_d = [&](int c, const v4i (&d)[kDig]) {
+    int8_t* dst = lds + (c & 1) * kN * kPitch;
+#pragma unroll
+    for (int i = 0; i < kDig; ++i) {
+      const int idx = threadIdx.x + i * kThreads;
+      const int n = idx / (kKC / 16), j = (idx % (kKC / 16)) * 16;
+      *reinterpret_cast<v4i*>(dst + n * kPitch + j) = d[i];
+    }
+  };
+  auto load_w = [&](int c, v4i (&a)[kU]) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int k = c * kKC + u * 64;
+      a[u] = k < kpad ? *reinterpret_cast<const v4i*>(wp + k) : v4i{0, 0, 0, 0};
+    }
+  };
+
+  v4i acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = v4i{0, 0, 0, 0};
+  v4i a_cur[kU], a_next[kU], d_next[kDig];
+  load_w(0, a_cur);
+  load_d(0, d_next);
+  store_d(0, d_next);
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    const bool more = c + 1 < nchunks;
+    if (more) {
+      load_w(c + 1, a_next);
+      load_d(c + 1, d_next);
+    }
+    const int8_t* buf = lds + (c & 1) * kN * kPitch;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const v4i b = *reinterpret_cast<const v4i*>(buf + (t * 16 + r_l) * kPitch + u * 64 + kg * 16);
+        acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_cur[u], b, acc[t], 0, 0, 0);
+      }
+    }
+    // Buffer (c + 1) & 1 was last read in iteration c - 1, before that iteration's barrier.
+    if (more) store_d(c + 1, d_next);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kU; ++u) a_cur[u] = a_next[u];
+  }
+
+  // C tile in LDS: [64 rows][kN] int32 (the digit buffers are no longer needed).
+  int* csum = reinterpret_cast<int*>(lds);
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) csum[(wave * 16 + 4 * kg + v) * kN + t * 16 + r_l] = acc[t][v];
+  __syncthreads();
+
+  for (int idx = threadIdx.x; idx < 64 * batch; idx += kThreads) {
+    const int r = idx / batch, b = idx % batch;
+    const int row = row0 + r;
+    const int* cr = csum + r * kN + 3 * b;
+    const int64_t sum = static_cast<int64_t>(cr[0]) + 256 * static_cast<int64_t>(cr[1]) + 65536 * static_cast<int64_t>(cr[2]);
+    const float y = static_cast<float>(sum) * pow2[b];
+    if constexpr (EPI == kEpiSwiglu) {
+      if ((r & 1) == 0 && row + 1 < rows) {
+        const int* cu = cr + kN;
+        const int64_t su = static_cast<int64_t>(cu[0]) + 256 * static_cast<int64_t>(cu[1]) + 65536 * static_cast<int64_t>(cu[2]);
+        const float yu = static_cast<float>(su) * pow2[b];
+        const float g = y * S[row];
+        const float u = yu * S[row + 1];
+        const float silu = g / (1.0f + expf(-g));
+        O[static_cast<int64_t>(b) * osb + static_cast<int64_t>(row >> 1) * osr] = silu * u;
+      }
+    } else if (row < rows) {
+      const float v = y * S[row];
+      float* o = O + static_cast<int64_t>(b) * osb + static_cast<int64_t>(row) * osr;
+      if (EPI == kEpiAdd) *o = *o + v;
+      else *o = v;
+      if constexpr (AMAX) {
+        const unsigned long long cand = (static_cast<unsigned long long>(order_key(v)) << 32) | static_cast<uint32_t>(row);
+        atomicMax(&best[b], cand);
+      }
+    }
+  }
+  if constexpr (AMAX) {
+    __syncthreads();
+    if (threadIdx.x < batch)
+      atomicMax(&amax[threadIdx.x * kArgmaxSlots + (blockIdx.x & (kArgmaxSlots - 1))], best[threadIdx.x]);
+  }
+}
+
+template <int NT>
+size_t rows64_smem() {
+  const size_t dig = 2 * static_cast<size_t>(Rows64<NT>::kN) * Rows64<NT>::kPitch;
+  const size_t cs = 64 * static_cast<size_t>(Rows64<NT>::kN) * 4;
+  return dig > cs ? dig : cs;
+}
+
+template <int NT, int EPI, bool AMAX>
+void go_rows64(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, const float* pow2, float* O,
+               int64_t osb, int64_t osr, int rows, int batch, int chunks, unsigned long long* amax, hipStream_t st) {
+  const size_t smem = rows64_smem<NT>();
+  static bool raised = false;
+  if (!raised && smem > 65536) {
+    PIA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_rows64<NT, EPI, AMAX>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
+    raised = true;
+  }
+  hipLaunchKernelGGL((k_gemm_rows64<NT, EPI, AMAX>), dim3((rows + 63) / 64, chunks), dim3(kThreads), smem, st, W, ldw,
+                     S, D, kpad, pow2, O, osb, osr, rows, batch, amax);
+}
+
 template <int NT>
 void go_dec(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, const float* pow2, float* O,
             int64_t osb, int64_t osr, int rows, int batch, int chunks, Epi epi, unsigned long long* amax,
             hipStream_t st) {
+  // Tall matrices: 64-row tiles with the digits shared through LDS (enough tiles to fill the
+  // CUs); short ones: 16-row tiles whose 4 wavefronts split K.
+  if (static_cast<int64_t>((rows + 63) / 64) * chunks >= 96) {
+    if (epi == Epi::Add) go_rows64<NT, kEpiAdd, false>(W, ldw, S, D, kpad, pow2, O, osb, osr, rows, batch, chunks, amax, st);
+    else if (epi == Epi::Swiglu)
+      go_rows64<NT, kEpiSwiglu, false>(W, ldw, S, D, kpad, pow2, O, osb, osr, rows, batch, chunks, amax, st);
+    else if (amax) go_rows64<NT, kEpiStore, true>(W, ldw, S, D, kpad, pow2, O, osb, osr, rows, batch, chunks, amax, st);
+    else go_rows64<NT, kEpiStore, false>(W, ldw, S, D, kpad, pow2, O, osb, osr, rows, batch, chunks, amax, st);
+    return;
+  }
   dim3 grid((rows + 15) / 16, chunks);
   if (epi == Epi::Add)
     hipLaunchKernelGGL((k_gemm_dec<NT, kEpiAdd, false>), grid, dim3(kThreads), 0, st, W, ldw, S, D, kpad, pow2, O, osb,

@@ -114,6 +114,7 @@ _SIGS = {
     "pia_model_prefill": (I32, [P, P, I64, I64, P, I64, P, P]),
     "pia_model_profile": (I32, [P, I32]),
     "pia_model_profile_get": (I32, [P, P, P, P, I32]),
+    "pia_model_bench_class": (I32, [P, I32, I64, I32, C.POINTER(C.c_double), C.POINTER(I64)]),
     "pia_bench_projection": (I32, [P, I64, I64, I64, I32, I32, C.POINTER(C.c_double), C.POINTER(I64)]),
     "pia_synth_normal": (I32, [U64, U64, F32, P, I64]),
     "pia_f32_to_bf16": (I32, [P, P, I64]),
@@ -485,6 +486,13 @@ class Model:
         check(lib().pia_model_prefill(self.h, ptr(tok), tok.size, start_pos, ptr(t), len(table), ptr(logits),
                                       ptr(am)))
         return logits, int(am[0])
+
+    def bench_class(self, cls: str, batch: int, reps: int = 5):
+        """(us per launch, algorithmic bytes per launch) of one projection class at `batch`."""
+        us, by = C.c_double(), I64()
+        check(lib().pia_model_bench_class(self.h, self.PROFILE_CLASSES.index(cls), batch, reps, C.byref(us),
+                                          C.byref(by)))
+        return us.value, by.value
 
     def profile(self, on: bool):
         check(lib().pia_model_profile(self.h, int(on)))
