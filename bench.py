@@ -32,6 +32,7 @@ METRIC = "int8 decode tok/s (B=1,32) + int8 GEMV HBM GB/s as % of ~8 TB/s peak"
 # WRITE_SIZE runs scaled by a 256 MiB copy (profiles/decode_b1_projection_traffic.md).
 TRAFFIC_GATE_UP_B1 = 23_420_000
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak, TOP/s
 SEED = 2024
 
 
@@ -65,8 +66,11 @@ def profile_pass(model, toks, pos, tables, steps):
     model.profile(True)
     n = len(pia.Model.PROFILE_CLASSES)
     acc, by, calls = np.zeros(n), np.zeros(n), np.zeros(n)
+    first_tokens, first_pos, first_argmax = list(toks), list(pos), None
     for _ in range(steps):
         _, am = model.decode(toks, pos, tables, want_logits=False)
+        if first_argmax is None:
+            first_argmax = am.tolist()
         ms, b, c = model.profile_get()
         acc += ms
         by += b
@@ -78,7 +82,8 @@ def profile_pass(model, toks, pos, tables, steps):
                   "us_per_launch": 1e3 * acc[i] / max(calls[i], 1), "launches_per_step": calls[i] / steps}
            for i, name in enumerate(pia.Model.PROFILE_CLASSES)}
     return dict(classes=per, gemv_ms=sum(acc[i] for i in range(5)) / steps, attn_ms=acc[5] / steps,
-                other_ms=acc[6] / steps, gemv_bytes=sum(by[i] for i in range(5)) / steps, attn_bytes=by[5] / steps)
+                other_ms=acc[6] / steps, gemv_bytes=sum(by[i] for i in range(5)) / steps, attn_bytes=by[5] / steps,
+                first_tokens=first_tokens, first_pos=first_pos, first_argmax=first_argmax)
 
 
 def run_b1(ctx, cfg, weights, steps, warmup, prompt_len=512):
@@ -144,13 +149,161 @@ def run_b32(ctx, cfg, weights, steps, warmup, batch=32):
     prof = profile_pass(model, toks, pos, tables, min(steps, 5))
     gemv_ms, attn_ms, gemv_bytes, attn_bytes = prof["gemv_ms"], prof["attn_ms"], prof["gemv_bytes"], prof["attn_bytes"]
     gu = prof["classes"]["gate_up"]
+    state = dict(toks=prof["first_tokens"], pos=prof["first_pos"], tables=tables, nb=nb,
+                 gpu_argmax=prof["first_argmax"],
+                 kv=model.kv_download() if os.environ.get("BENCH_CPU", "1") == "1" else None)
     model.close()
-    return dict(tok_s=batch * steps / elapsed, ms_per_step=1e3 * elapsed / steps,
+    return state, dict(tok_s=batch * steps / elapsed, ms_per_step=1e3 * elapsed / steps,
                 prefill_tok_s=float(np.sum(ctxs)) / prefill_s, mean_ctx=float(np.mean(ctxs)),
                 gemv_gbs=(gemv_bytes / 1e9) / (gemv_ms / 1e3) if gemv_ms else None,
                 attn_gbs=(attn_bytes / 1e9) / (attn_ms / 1e3) if attn_ms else None,
                 gemv_ms=gemv_ms, attn_ms=attn_ms,
                 gate_up_gbs=gu["bytes_per_launch"] / (gu["us_per_launch"] * 1e3))
+
+
+def run_c4_prefill(ctx, cfg, weights, seqs=8, seq_len=2048):
+    """`seqs` sequences of `seq_len` uniform-random tokens prefilled one after the
+    other (prefill_batched per sequence, src/model.rs:1222-1255), each into its own block table
+    drawn from a random permutation of the pool. Reports prompt tokens/s and the matrix-core
+    utilisation of the projection GEMMs (useful int8 ops 2*M*rows*cols over their device time)."""
+    bs = 16
+    nbs = (seq_len + bs - 1) // bs
+    rng = np.random.default_rng(SEED + 4)
+    perm = rng.permutation(seqs * nbs).tolist()
+    tables = [perm[i * nbs:(i + 1) * nbs] for i in range(seqs)]
+    prompts = [rng.integers(0, cfg.vocab, seq_len).tolist() for _ in range(seqs)]
+    model = pia.Model(ctx, cfg, weights)
+    model.kv_alloc(seqs * nbs, bs)
+    model.prefill(prompts[0][:256], 0, tables[0], want_logits=False)  # warm-up (allocations, code load)
+    ctx.sync()
+    t0 = time.perf_counter()
+    first = [model.prefill(p, 0, t, want_logits=False)[1] for p, t in zip(prompts, tables)]
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    # Per-class device time of one more prefill of sequence 0 (same inputs, eager, HIP events).
+    model.profile(True)
+    model.prefill(prompts[0], 0, tables[0], want_logits=False)
+    ms, _, calls = model.profile_get()
+    model.profile(False)
+    hd = cfg.head_dim
+    kvd = cfg.kv_heads * hd
+    per_layer = {"qkv": (cfg.hidden + 2 * kvd) * cfg.hidden, "o": cfg.hidden * cfg.hidden,
+                 "gate_up": 2 * cfg.inter * cfg.hidden, "down": cfg.hidden * cfg.inter}
+    names = pia.Model.PROFILE_CLASSES
+    proj_ops = sum(2.0 * seq_len * per_layer[k] * cfg.layers for k in per_layer)
+    proj_ms = sum(ms[names.index(k)] for k in per_layer)
+    classes = {}
+    for k in per_layer:
+        i = names.index(k)
+        ops = 2.0 * seq_len * per_layer[k] * cfg.layers
+        classes[k] = {"ms": round(ms[i], 3), "TOP/s": round(ops / (ms[i] * 1e-3) / 1e12, 1)}
+    classes["attention"] = {"ms": round(ms[names.index("attention")], 3)}
+    classes["other"] = {"ms": round(ms[names.index("other")], 3)}
+    achieved = proj_ops / (proj_ms * 1e-3) / 1e12
+    model.close()
+    return dict(tok_s=seqs * seq_len / elapsed, ms_per_seq=1e3 * elapsed / seqs, first_tokens=first,
+                gemm_tops=achieved, gemm_frac=achieved / INT8_PEAK_TOPS, classes=classes,
+                tables=tables, prompts=prompts)
+
+
+def run_c5(ctx, steps, warmup, seed=SEED + 5):
+    """Llama-3-8B-shaped int8 decode at batch 64 with prefix sharing and COW.
+
+    Per prefix group g (4 groups of one random 1024-token prefix): 8 parent sequences admit
+    prefix_g + an 8-token parent tail through the KvCacheManager's PrefixCache (the first
+    misses and prefills 1032 tokens, then publishes the 64 full prefix blocks; the other 7 hit
+    them and prefill only their 8 tail tokens); each parent forks 2 children, which share the
+    parent's partially filled tail block; each child then writes its 256 unique random prompt
+    tokens starting mid-block, so ensure_writable copies the shared tail block (copy-on-write,
+    on the device) before the child's prefill. Parents are released; the 64 children decode
+    `steps` greedy steps at batch 64. Returns tok/s plus the state needed by the CPU leg."""
+    cfg = pia.LLAMA3_8B
+    bs, groups, parents, kids, prefix_len, tail_len, uniq = 16, 4, 8, 2, 1024, 8, 256
+    log("synthesizing Llama-3-8B-shape int8 weights")
+    weights = pia.synth_weights(cfg, seed=seed)
+    rng = np.random.default_rng(seed)
+    n_child = groups * parents * kids
+    prompt_total = prefix_len + tail_len + uniq
+    per_child = (prompt_total + warmup + steps + 2 * bs) // bs + 1
+    total_blocks = groups * (prefix_len // bs + parents) + n_child * per_child
+    model = pia.Model(ctx, cfg, weights)
+    model.kv_alloc(total_blocks, bs)
+    kvm = pia.KvCacheManager(total_blocks, bs, prefix_cache=True)
+    tick = 0
+    t0 = time.perf_counter()
+    prefill_tokens = 0
+    children = []  # (seq_id, Table, prompt)
+    parent_ids = []
+    for g in range(groups):
+        prefix = rng.integers(0, cfg.vocab, prefix_len).tolist()
+        for p in range(parents):
+            pid = 1000 + g * parents + p
+            tail = rng.integers(0, cfg.vocab, tail_len).tolist()
+            toks = prefix + tail
+            tick += 1
+            got = kvm.admit(pid, toks, tick)
+            assert got is not None, "KV pool too small for the c5 workload"
+            table, (cached, _, _) = got
+            model.prefill(toks[cached:], cached, table.blocks(), want_logits=False)
+            prefill_tokens += len(toks) - cached
+            kvm.publish(table)
+            parent_ids.append(pid)
+            for k in range(kids):
+                cid = g * parents * kids + p * kids + k
+                tick += 1
+                ct = kvm.fork(table, cid, tick)
+                children.append((cid, ct, toks + rng.integers(0, cfg.vocab, uniq).tolist()))
+    # Children: copy-on-write of the shared tail block, then prefill of the unique tokens.
+    first = []
+    for cid, ct, toks in children:
+        pos0 = prefix_len + tail_len
+        kvm.ensure_writable(cid, ct, pos0, ctx, model.kv_ptr, model.layout)
+        while len(ct) * bs < prompt_total:
+            tick += 1
+            assert kvm.append_block(cid, ct, tick)
+        _, t = model.prefill(toks[pos0:], pos0, ct.blocks(), want_logits=False)
+        prefill_tokens += uniq
+        first.append(t)
+    ctx.sync()
+    prefill_s = time.perf_counter() - t0
+    for pid in parent_ids:
+        kvm.release(pid)
+    # Map every block the decode steps will write (append_block on the same manager).
+    for cid, ct, _ in children:
+        while len(ct) * bs < prompt_total + warmup + 2 * steps + 8:
+            tick += 1
+            assert kvm.append_block(cid, ct, tick)
+    stats = kvm.stats()
+    tables = [ct.blocks() for _, ct, _ in children]
+    toks, pos = decode_loop(model, first, [prompt_total] * n_child, tables, warmup, bs)
+    ctx.sync()
+    t0 = time.perf_counter()
+    toks, pos = decode_loop(model, toks, pos, tables, steps, bs)
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    prof = profile_pass(model, toks, pos, tables, 3)
+    # Logical KV bytes one decode step reads (every entry's mapped window, all layers) and the
+    # compulsory bytes (each distinct physical block read once).
+    distinct = set()
+    logical = 0
+    for t, p in zip(tables, pos):
+        nb_used = p // bs + 1
+        distinct.update(t[:nb_used])
+        logical += (p + 1) * cfg.layers * cfg.kv_heads * 2 * cfg.head_dim * 4
+    compulsory = len(distinct) * bs * cfg.layers * cfg.kv_heads * 2 * cfg.head_dim * 4
+    res = dict(tok_s=n_child * steps / elapsed, ms_per_step=1e3 * elapsed / steps, batch=n_child, steps=steps,
+               prefill_tok_s=prefill_tokens / prefill_s, prefill_tokens=prefill_tokens,
+               weight_bytes=model.weight_bytes(), kv_logical_bytes_per_step=logical,
+               kv_compulsory_bytes_per_step=compulsory,
+               gemv_ms=prof["gemv_ms"], attn_ms=prof["attn_ms"], other_ms=prof["other_ms"],
+               gemv_gbs=(prof["gemv_bytes"] / 1e9) / (prof["gemv_ms"] / 1e3),
+               attn_logical_gbs=(logical / 1e9) / (prof["attn_ms"] / 1e3),
+               prefix_cache={k: stats[k] for k in ("hits", "misses", "inserts", "tokens_saved", "cow_copies")},
+               first_argmax=prof["first_argmax"])
+    state = dict(cfg=cfg, weights=weights, toks=prof["first_tokens"], pos=prof["first_pos"], tables=tables,
+                 nb=total_blocks, kv=model.kv_download() if os.environ.get("BENCH_CPU", "1") == "1" else None)
+    model.close()
+    return res, state
 
 
 SWEEP_SHAPES = [  # (name, rows, cols) of the fused projections
@@ -169,32 +322,57 @@ def gemv_sweep(ctx, batch=1, reps=20):
     return out
 
 
-def cpu_baseline(cfg, weights, b1, kv_state, budget_s=15.0):
-    """The oracle (C++ restatement of the reference's rayon + AVX2 path) decoding at batch 1
-    from the GPU run's KV state, on this host's cores, for a bounded number of steps."""
+def cpu_decode_baseline(cfg, weights, toks, pos, tables, nb, kv, gpu_argmax, budget_s, label):
+    """The oracle decoding one batch step after another from the GPU run's KV state (same
+    tokens, positions and block tables), on this host's cores, for about `budget_s` seconds.
+    Also checks the first step's greedy tokens against the GPU's for the same inputs."""
     sys.path.insert(0, str(ROOT))
     from oracle import oracle as orc
     cores = host_cores()
     orc.set_threads(cores)
     om = orc.OracleModel(cfg, weights)
-    tok, pos, table, nb = b1["last_tok"], b1["last_pos"], b1["table"], b1["nb"]
-    kv = kv_state
+    b = len(toks)
     t0 = time.perf_counter()
-    lc = om.decode([tok], [pos], [table], kv, nb, 16)
+    lc = om.decode(toks, pos, tables, kv, nb, 16)
     one = time.perf_counter() - t0
-    n = int(max(2, min(200, budget_s / max(one, 1e-3))))
-    tok = orc.argmax(lc[0])
-    pos += 1
-    t0 = time.perf_counter()
+    first = [orc.argmax(lc[i]) for i in range(b)]
+    match = sum(int(x == int(y)) for x, y in zip(first, gpu_argmax))
+    n = int(max(1, min(200, budget_s / max(one, 1e-3)))) - 1
+    tk, ps = first, [p + 1 for p in pos]
+    t1 = time.perf_counter()
     for _ in range(n):
-        lc = om.decode([tok], [pos], [table], kv, nb, 16)
-        tok = orc.argmax(lc[0])
-        pos += 1
+        lc = om.decode(tk, ps, tables, kv, nb, 16)
+        tk = [orc.argmax(lc[i]) for i in range(b)]
+        ps = [p + 1 for p in ps]
+    el = (time.perf_counter() - t1) if n else one
+    steps = n if n else 1
+    return {"value": b * steps / el, "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{steps} greedy decode steps at batch {b} ({label}) from the GPU run's KV state, "
+                      f"oracle/ref_cpu.cpp with {cores} threads, avx2={bool(orc.lib().orc_have_avx2())}",
+            "first_step_argmax_match": f"{match}/{b}"}
+
+
+def cpu_prefill_baseline(cfg, weights, prompt, budget_s=10.0):
+    """The oracle's prefill_batched (32-token chunks, as the reference) over the first tokens of
+    one configs[3] prompt, for about `budget_s` seconds."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as orc
+    cores = host_cores()
+    orc.set_threads(cores)
+    om = orc.OracleModel(cfg, weights)
+    nb = len(prompt) // 16 + 1
+    kv = np.zeros(orc.kv_floats(cfg, nb, 16), np.float32)
+    table = list(range(nb))
+    t0 = time.perf_counter()
+    om.prefill(prompt[:32], 0, table, kv, nb, 16)
+    one = time.perf_counter() - t0
+    n = int(max(1, min(len(prompt) // 32 - 1, budget_s / max(one, 1e-3))))
+    t0 = time.perf_counter()
+    om.prefill(prompt[32:32 + 32 * n], 32, table, kv, nb, 16)
     el = time.perf_counter() - t0
-    return {"value": n / el, "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{n} greedy decode steps at batch 1 (TinyLlama shape, int8 incl. lm_head) from the GPU "
-                      f"run's KV state at position {b1['last_pos']}, oracle/ref_cpu.cpp with {cores} threads, "
-                      f"avx2={bool(orc.lib().orc_have_avx2())}"}
+    return {"value": 32 * n / el, "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"prefill of prompt tokens 32..{32 + 32 * n} of one configs[3] sequence (32-token chunks), "
+                      f"oracle/ref_cpu.cpp with {cores} threads"}
 
 
 def main():
@@ -202,7 +380,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--no-b32", action="store_true")
+    ap.add_argument("--no-b32", action="store_true", help="skip configs[2] (batch-32 paged decode)")
+    ap.add_argument("--no-c4", action="store_true", help="skip configs[3] (8 x 2048-token prefill)")
+    ap.add_argument("--no-c5", action="store_true", help="skip configs[4] (Llama-3-8B batch 64, prefix + COW)")
+    ap.add_argument("--c5-steps", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep", action="store_true", help="also time each projection shape alone")
     ap.add_argument("--only-b32", action="store_true", help="run only the batch-32 decode (profiling aid)")
@@ -215,10 +396,9 @@ def main():
         sys.exit(2)
     if args.no_cpu:
         os.environ["BENCH_CPU"] = "0"
+    cpu = not args.no_cpu
 
     cfg = pia.TINYLLAMA
-    log("building synthetic TinyLlama int8 weights")
-    weights = pia.synth_weights(cfg, seed=SEED)
     ctx = pia.Context(0)
     if args.copy_calibration:
         lay = pia.KvLayout(1, 2, 32768, 8, 128)  # one block = 32768*8*2*128 floats = 256 MiB
@@ -228,8 +408,10 @@ def main():
         ctx.sync()
         print(json.dumps({"copy_calibration": {"bytes_read": 1 << 28, "bytes_written": 1 << 28, "launches": 3}}))
         return
+    log("building synthetic TinyLlama int8 weights")
+    weights = pia.synth_weights(cfg, seed=SEED)
     if args.only_b32:
-        b32 = run_b32(ctx, cfg, weights, args.steps, args.warmup)
+        _, b32 = run_b32(ctx, cfg, weights, args.steps, args.warmup)
         print(json.dumps({"b32": b32}), flush=True)
         return
     log("B=1 decode")
@@ -264,16 +446,49 @@ def main():
         "projections_b1": b1["launch"],
         "step_breakdown_ms": {k: round(v["ms_per_step"], 4) for k, v in b1["classes"].items()},
     }
+    if cpu:
+        log("CPU baseline (batch 1)")
+        out["cpu_baseline"] = cpu_decode_baseline(cfg, weights, b1["first_tokens"], b1["first_pos"], [b1["table"]],
+                                                  b1["nb"], kv_state, b1["first_argmax"], 15.0,
+                                                  "TinyLlama shape, int8 incl. lm_head")
+        kv_state = None
     if not args.no_b32:
-        log("B=32 paged decode")
-        b32 = run_b32(ctx, cfg, weights, max(5, args.steps // 4), max(2, args.warmup // 2))
+        log("B=32 paged decode (configs[2])")
+        st32, b32 = run_b32(ctx, cfg, weights, max(5, args.steps // 4), max(2, args.warmup // 2))
         out["b32"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in b32.items()}
+        if cpu:
+            log("CPU baseline (batch 32)")
+            out["b32"]["cpu_baseline"] = cpu_decode_baseline(cfg, weights, st32["toks"], st32["pos"], st32["tables"],
+                                                             st32["nb"], st32["kv"], st32["gpu_argmax"], 10.0,
+                                                             "TinyLlama shape, configs[2] contexts and tables")
+        st32 = None
+    if not args.no_c4:
+        log("8 x 2048-token prefill (configs[3])")
+        c4 = run_c4_prefill(ctx, cfg, weights)
+        prompt0 = c4.pop("prompts")[0]
+        c4.pop("tables")
+        out["c4_prefill"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c4.items()}
+        out["c4_prefill"]["mfma_roofline"] = {"bound": "mfma", "achieved": round(c4["gemm_tops"], 1),
+                                              "peak": INT8_PEAK_TOPS, "unit": "TOP/s (useful int8 ops)",
+                                              "frac": round(c4["gemm_frac"], 4)}
+        if cpu:
+            log("CPU baseline (prefill)")
+            out["c4_prefill"]["cpu_baseline"] = cpu_prefill_baseline(cfg, weights, prompt0)
     if args.sweep:
         log("GEMV shape sweep")
         out["gemv_sweep_b1"] = gemv_sweep(ctx, 1)
-    if not args.no_cpu:
-        log("CPU baseline")
-        out["cpu_baseline"] = cpu_baseline(cfg, weights, b1, kv_state)
+    weights = None
+    if not args.no_c5:
+        log("Llama-3-8B batch-64 decode with prefix sharing + COW (configs[4])")
+        c5, st5 = run_c5(ctx, args.c5_steps, 4)
+        out["c5_llama3_8b_b64"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c5.items()}
+        if cpu:
+            log("CPU baseline (Llama-3-8B batch 64)")
+            out["c5_llama3_8b_b64"]["cpu_baseline"] = cpu_decode_baseline(
+                st5["cfg"], st5["weights"], st5["toks"], st5["pos"], st5["tables"], st5["nb"], st5["kv"],
+                c5["first_argmax"], 20.0, "Llama-3-8B shape, configs[4] prefix-shared tables")
+        out["c5_llama3_8b_b64"].pop("first_argmax")
+        st5 = None
     ctx.close()
     print(json.dumps(out), flush=True)
 
