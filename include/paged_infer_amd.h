@@ -224,9 +224,18 @@ pia_status pia_model_decode(pia_model* m, const uint32_t* tokens, const int64_t*
 pia_status pia_model_prefill(pia_model* m, const uint32_t* tokens, int64_t n, int64_t start_pos,
                              const int32_t* table, int64_t table_len, float* logits, int32_t* argmax);
 
+/* Decode path. 0 (default): one launch per kernel. 1: a batch-1 decode runs as one persistent
+ * launch (every layer and the LM head, one workgroup per CU, stages separated by grid
+ * barriers) when every projection is int8 and the shape fits, else one launch per kernel.
+ * pia_model_decode_path_used reports the path of the last pia_model_decode (0 per-kernel,
+ * 1 persistent, -1 none yet). No counterpart in the reference (it has no GPU int8 path). */
+pia_status pia_model_set_decode_path(pia_model* m, int32_t path);
+int32_t pia_model_decode_path_used(const pia_model* m);
+
 /* Per-kernel timing of the last pia_model_decode / pia_model_prefill call (HIP events around
  * every launch on the context stream), accumulated per class: 0 = q/k/v projection, 1 = o,
- * 2 = gate/up, 3 = down, 4 = LM head, 5 = attention, 6 = everything else. `bytes` are the
+ * 2 = gate/up, 3 = down, 4 = LM head, 5 = attention, 6 = everything else, 7 = the persistent
+ * batch-1 decode step (all of a step in one launch). `bytes` are the
  * algorithmic bytes of those launches, `calls` their number. Enable with
  * pia_model_profile(m, 1); profiled calls run without graph replay. No counterpart in the
  * reference (its benches time whole steps). */

@@ -9,6 +9,8 @@
 #include <array>
 #include <cmath>
 #include <map>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -49,7 +51,7 @@ struct Prof {
   std::vector<hipEvent_t> pool;
   std::vector<Rec> recs;
   size_t used = 0;
-  static constexpr int kClasses = 7;
+  static constexpr int kClasses = 8;
   double ms[kClasses] = {};
   int64_t bytes[kClasses] = {};
   int64_t calls[kClasses] = {};
@@ -97,6 +99,14 @@ struct pia_model {
   int64_t mfma_min = kMfmaMinBatch;
   PinnedBuffer pin, pin_out;
   Prof prof;
+
+  // Persistent batch-1 decode step (decode_step.hip).
+  int decode_path = 0;        // 0: per-kernel launches, 1: persistent step at batch 1 when the shape allows
+  int last_path = -1;         // path of the last decode: 0 per-kernel launches, 1 persistent step
+  int step_state = -1;        // -1 not checked since the last weight change, 0 unsupported, 1 ready
+  bool step_disabled = false;  // a grid barrier timed out: per-kernel launches from then on
+  StepShape step_shape{};
+  DeviceBuffer step_layers, step_part, step_ctrl, step_trace;  // ctrl: flags[num_cus * 32], step counter, error flag
 
   // Replayable decode / prefill steps. Every kernel argument is a device pointer into the
   // buffers above, so a graph stays valid until one of them is reallocated.
@@ -180,6 +190,16 @@ struct pia_model {
     const int64_t wb = p.kind == 1 ? p.rows * p.cols + 4 * p.rows : 4 * p.rows * p.cols;
     const int64_t outr = epi == Epi::Swiglu ? p.rows / 2 : p.rows;
     return wb + 4 * batch * p.cols + 4 * batch * outr;
+  }
+
+  // Algorithmic bytes of one persistent decode step: every projection's weights and scales
+  // read once, the K/V of the mapped window, and the activations of each stage.
+  int64_t step_bytes(int64_t mapped_tokens) const {
+    int64_t b = proj_bytes(lm_head, 1, Epi::Store);
+    for (const auto& L : layers)
+      b += proj_bytes(L.qkv, 1, Epi::Store) + proj_bytes(L.o, 1, Epi::Add) + proj_bytes(L.gu, 1, Epi::Swiglu) +
+           proj_bytes(L.down, 1, Epi::Add);
+    return b + cfg.layers * (mapped_tokens * cfg.kv_heads * 2 * hd * 4 + 2 * cfg.hidden * 4);
   }
 
   // Profiling classes (pia_model_profile_get): projections by role, attention, the rest.
@@ -272,13 +292,118 @@ struct pia_model {
     }
   }
 
+  // Whether the persistent step kernel runs this model's batch-1 decode (checked once per
+  // weight change; builds the device array of layer pointers it reads).
+  bool step_ready() {
+    if (decode_path != 1 || step_disabled || cfg.attention_window == 0) return false;
+    if (step_state >= 0) return step_state == 1;
+    step_state = 0;
+    if (lm_head.kind != 1) return false;
+    for (const auto& L : layers)
+      if (L.qkv.kind != 1 || L.o.kind != 1 || L.gu.kind != 1 || L.down.kind != 1) return false;
+    const int ncu = ctx->num_cus;
+    StepShape s{};
+    s.hidden = cfg.hidden, s.heads = cfg.heads, s.hkv = cfg.kv_heads, s.hd = hd, s.inter = cfg.inter;
+    s.vocab = cfg.vocab, s.qkv_rows = qkv_rows, s.lm_i8 = true;
+    s.max_splits = decode_step_splits(ncu, cfg.kv_heads);
+    const int64_t g = cfg.heads / cfg.kv_heads;
+    s.max_tokens = std::min<int64_t>(2048, (static_cast<int64_t>(kMaxStepSmem) / 4 - g * hd - 2 * hd - 2 * g) / (1 + g));
+    if (s.max_tokens < 16 || decode_step_unsupported(s, ncu)) return false;
+    std::vector<StepLayer> v(cfg.layers);
+    for (int64_t l = 0; l < cfg.layers; ++l) {
+      const Layer& L = layers[l];
+      v[l] = StepLayer{static_cast<const int8_t*>(L.qkv.w.ptr), L.qkv.s.as<float>(),
+                       static_cast<const int8_t*>(L.o.w.ptr),   L.o.s.as<float>(),
+                       static_cast<const int8_t*>(L.gu.w.ptr),  L.gu.s.as<float>(),
+                       static_cast<const int8_t*>(L.down.w.ptr), L.down.s.as<float>(),
+                       L.attn_norm.as<float>(),                  L.ffn_norm.as<float>()};
+    }
+    grow(step_layers, v.size() * sizeof(StepLayer));
+    PIA_HIP(hipMemcpy(step_layers.ptr, v.data(), v.size() * sizeof(StepLayer), hipMemcpyHostToDevice));
+    grow(step_part, static_cast<size_t>(cfg.heads) * s.max_splits * (hd + 2) * 4);
+    const size_t ctrl = (static_cast<size_t>(ncu) * 32 + 64 + cfg.kv_heads * 32) * 4;
+    if (step_ctrl.bytes < ctrl) {
+      grow(step_ctrl, ctrl);
+      PIA_HIP(hipMemset(step_ctrl.ptr, 0, ctrl));
+    }
+    if (std::getenv("PIA_STEP_TRACE")) grow(step_trace, (32 * cfg.layers + 4) * 8);
+    step_shape = s;
+    step_state = 1;
+    return true;
+  }
+  // PIA_STEP_TRACE=1: mean device-clock microseconds of each stage of the last step, to stderr.
+  void print_step_trace() {
+    const int64_t n = 16 * cfg.layers + 2;
+    std::vector<unsigned long long> t(2 * n);
+    PIA_HIP(hipMemcpy(t.data(), step_trace.ptr, 2 * n * 8, hipMemcpyDeviceToHost));
+    PIA_HIP(hipMemset(step_trace.ptr, 0, 2 * n * 8));
+    int khz = 100000;
+    (void)hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, ctx->device);
+    const double us = 1e3 / khz;
+    // Per stage (A qkv, B attention, D o, E gate/up, F down): WG 0's start, the latest
+    // arrival of any workgroup at the stage's barrier, WG 0's exit from it.
+    const int start[5] = {0, 2, 6, 9, 12}, arrive[5] = {1, 3, 8, 11, 14}, exitm[5] = {2, 4, 9, 12, -1};
+    static const char* names[5] = {"A.qkv", "B.attn", "D.o", "E.gu", "F.down"};
+    double work[5] = {}, bar[5] = {};
+    for (int64_t l = 1; l < cfg.layers; ++l)
+      for (int k = 0; k < 5; ++k) {
+        const unsigned long long s0 = t[16 * l + start[k]], a = t[n + 16 * l + arrive[k]];
+        const unsigned long long e = exitm[k] >= 0 ? t[16 * l + exitm[k]] : (l + 1 < cfg.layers ? t[16 * (l + 1)] : t[16 * cfg.layers]);
+        work[k] += static_cast<double>(static_cast<long long>(a - s0)) * us;
+        bar[k] += static_cast<double>(static_cast<long long>(e - a)) * us;
+      }
+    std::fprintf(stderr, "[step trace] per layer (us): slowest-WG work / barrier exit after last arrival:");
+    for (int k = 0; k < 5; ++k)
+      std::fprintf(stderr, " %s=%.2f/%.2f", names[k], work[k] / (cfg.layers - 1), bar[k] / (cfg.layers - 1));
+    std::fprintf(stderr, " | LM=%.2f total=%.1f\n", static_cast<double>(t[n - 1] - t[n - 2]) * us,
+                 static_cast<double>(t[n - 1] - t[0]) * us);
+  }
+  unsigned* step_flags() const { return step_ctrl.as<unsigned>(); }
+  unsigned* step_counter() const { return step_ctrl.as<unsigned>() + ctx->num_cus * 32; }
+  int* step_err() const { return reinterpret_cast<int*>(step_ctrl.as<unsigned>() + ctx->num_cus * 32 + 32); }
+
+  // decode_batch_into at batch 1 as one launch (see decode_step.hip).
+  void launch_step(const StepDev& in) {
+    StepParams p{};
+    p.layers = static_cast<int>(cfg.layers), p.hidden = static_cast<int>(cfg.hidden);
+    p.heads = static_cast<int>(cfg.heads), p.hkv = static_cast<int>(cfg.kv_heads);
+    p.inter = static_cast<int>(cfg.inter), p.vocab = static_cast<int>(cfg.vocab);
+    p.qkv_rows = static_cast<int>(qkv_rows);
+    p.ld_h = layers[0].qkv.ld, p.ld_i = layers[0].down.ld, p.ld_lm = lm_head.ld;
+    p.eps = cfg.rms_eps, p.scale = 1.0f / sqrtf(static_cast<float>(hd));
+    p.L = step_layers.as<StepLayer>();
+    p.lm = lm_head.w.ptr, p.lm_s = lm_head.s.as<float>();
+    p.final_norm = final_norm.as<float>(), p.embed = embed.as<uint16_t>();
+    p.kv = kv.as<float>(), p.num_blocks = static_cast<int>(layout.num_blocks);
+    p.block_size = static_cast<int>(layout.block_size);
+    p.rope_cos = rope_cos.as<float>(), p.rope_sin = rope_sin.as<float>();
+    p.token = in.tokens, p.entry = in.entries, p.tables = in.tables;
+    p.x = x.as<float>(), p.qkv_buf = qkv.as<float>(), p.attn = attn.as<float>(), p.h = h.as<float>();
+    p.part = step_part.as<float>(), p.logits = logits.as<float>(), p.amax = amax.as<unsigned long long>();
+    p.flags = step_flags(), p.step_ctr = step_counter(), p.err = step_err();
+    p.attn_cnt = step_counter() + 64;
+    p.max_splits = static_cast<int>(step_shape.max_splits);
+    p.trace = step_trace.as<unsigned long long>();
+    launch_decode_step(p, step_shape, ctx->num_cus, st());
+  }
+
   // Copy the fused-argmax slots back, take the max of each row's slots (the low 32 bits are
   // the winning row) and wait for the step.
-  void read_argmax(int32_t* out, int64_t batch) {
+  void read_argmax(int32_t* out, int64_t batch, bool step = false) {
     const size_t bytes = batch * kArgmaxSlots * 8;
-    pin_out.ensure(bytes);
+    pin_out.ensure(bytes + 64);
     PIA_HIP(hipMemcpyAsync(pin_out.ptr, amax.ptr, bytes, hipMemcpyDeviceToHost, st()));
+    int* err_h = reinterpret_cast<int*>(static_cast<char*>(pin_out.ptr) + bytes);
+    if (step) PIA_HIP(hipMemcpyAsync(err_h, step_err(), 4, hipMemcpyDeviceToHost, st()));
     PIA_HIP(hipStreamSynchronize(st()));
+    if (step && *err_h) {
+      // A grid barrier ran out of its spin budget (the grid was not co-resident): the step's
+      // results are void. Later steps use per-kernel launches.
+      PIA_HIP(hipMemset(step_err(), 0, 4));
+      step_disabled = true;
+      drop_graphs();
+      fail(PIA_ERR_HIP, "persistent decode step: grid barrier timed out; per-kernel launches from now on");
+    }
     const auto* v = static_cast<const unsigned long long*>(pin_out.ptr);
     if (out)
       for (int64_t b = 0; b < batch; ++b) {
@@ -409,6 +534,9 @@ void set_proj(pia_model* m, int64_t layer, int32_t which, int kind, const void* 
                 "fused projection group mixes int8 and f32 slots; set every slot of the group with one kind");
     alloc_proj(*t.p, kind, total_rows(m, t.p), t.cols);
   }
+  PIA_HIP(hipStreamSynchronize(m->st()));
+  m->drop_graphs();  // a re-allocated projection moves; the step kernel's pointer table too
+  m->step_state = -1;
   upload_rows(*t.p, t.r0, t.rows, t.row_step, data, scales);
   t.p->filled |= t.bit;
 }
@@ -454,6 +582,8 @@ pia_status pia_model_set_embedding(pia_model* m, const uint16_t* bf16) {
   PIA_API_BEGIN
   PIA_REQUIRE(m && bf16, "null argument");
   const size_t bytes = static_cast<size_t>(m->cfg.vocab) * m->cfg.hidden * 2;
+  PIA_HIP(hipStreamSynchronize(m->st()));
+  m->drop_graphs();
   m->embed.ensure(bytes);
   PIA_HIP(hipMemcpy(m->embed.ptr, bf16, bytes, hipMemcpyHostToDevice));
   m->embed_set = true;
@@ -472,6 +602,9 @@ pia_status pia_model_set_norm(pia_model* m, int64_t layer, int32_t which, const 
     PIA_REQUIRE(which == PIA_NORM_ATTN || which == PIA_NORM_FFN, "unknown norm slot");
     dst = which == PIA_NORM_ATTN ? &m->layers[layer].attn_norm : &m->layers[layer].ffn_norm;
   }
+  PIA_HIP(hipStreamSynchronize(m->st()));
+  m->drop_graphs();
+  m->step_state = -1;
   dst->ensure(m->cfg.hidden * 4);
   PIA_HIP(hipMemcpy(dst->ptr, w, m->cfg.hidden * 4, hipMemcpyHostToDevice));
   PIA_API_END
@@ -507,6 +640,8 @@ pia_status pia_model_kv_alloc(pia_model* m, int64_t num_blocks, int64_t block_si
   PIA_HIP(hipSetDevice(m->ctx->device));
   m->layout = pia_kv_layout{m->cfg.layers, num_blocks, block_size, m->cfg.kv_heads, m->hd};
   const size_t bytes = static_cast<size_t>(m->cfg.layers) * num_blocks * block_size * m->cfg.kv_heads * 2 * m->hd * 4;
+  PIA_HIP(hipStreamSynchronize(m->st()));
+  m->drop_graphs();  // captured steps hold the old cache address
   m->kv.release();
   m->kv.ensure(bytes);
   PIA_HIP(hipMemset(m->kv.ptr, 0, bytes));
@@ -520,6 +655,21 @@ pia_status pia_model_kv(pia_model* m, float** kv, pia_kv_layout* layout) {
   if (layout) *layout = m->layout;
   PIA_API_END
 }
+
+pia_status pia_model_set_decode_path(pia_model* m, int32_t path) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(m, "null model");
+  PIA_REQUIRE(path == 0 || path == 1, "decode path must be 0 (per-kernel launches) or 1 (persistent step)");
+  if (path != m->decode_path) {
+    PIA_HIP(hipStreamSynchronize(m->st()));
+    m->drop_graphs();
+    m->decode_path = path;
+    m->step_state = -1;
+  }
+  PIA_API_END
+}
+
+int32_t pia_model_decode_path_used(const pia_model* m) { return m ? m->last_path : -1; }
 
 pia_status pia_model_profile(pia_model* m, int32_t enable) {
   PIA_API_BEGIN
@@ -708,16 +858,26 @@ pia_status pia_model_decode(pia_model* m, const uint32_t* tokens, const int64_t*
   m->grow(m->logits, batch * m->ld_v * 4);
   const int64_t wb = attention_work_bytes(batch, c.heads, m->hd, plan.splits);
   if (wb) m->grow(m->attn_work, wb);
+  const bool step = batch == 1 && m->step_ready() &&
+                    max_window <= m->step_shape.max_splits * m->step_shape.max_tokens;
   const pia_model::StepDev in = upload_step(m, tok, ent, tables, ntab);
-  m->run_step({0, batch, plan.split, plan.splits, plan.chunk, fused ? 1 : 0}, true, [&] {
-    m->run_layers(batch, in, plan, fused, mapped);
-    m->normed_gemv(m->lm_head, m->x.as<float>(), m->final_norm.as<float>(), batch, m->logits.as<float>(), m->ld_v,
-                   Epi::Store, m->amax.as<unsigned long long>());
-  });
+  if (step) {
+    m->run_step({2, 1, 0, 0, 0, 0}, true, [&] {
+      m->timed(7, m->step_bytes(mapped), [&] { m->launch_step(in); });
+    });
+  } else {
+    m->run_step({0, batch, plan.split, plan.splits, plan.chunk, fused ? 1 : 0}, true, [&] {
+      m->run_layers(batch, in, plan, fused, mapped);
+      m->normed_gemv(m->lm_head, m->x.as<float>(), m->final_norm.as<float>(), batch, m->logits.as<float>(), m->ld_v,
+                     Epi::Store, m->amax.as<unsigned long long>());
+    });
+  }
   if (logits)
     PIA_HIP(hipMemcpy2DAsync(logits, c.vocab * 4, m->logits.ptr, m->ld_v * 4, c.vocab * 4, batch,
                              hipMemcpyDeviceToHost, m->st()));
-  m->read_argmax(argmax, batch);
+  m->last_path = step ? 1 : 0;
+  m->read_argmax(argmax, batch, step);
+  if (step && m->step_trace.ptr) m->print_step_trace();
   m->finish_prof();
   PIA_API_END
 }

@@ -115,6 +115,64 @@ void launch_argmax(const float* logits, int64_t ld, int32_t* out, int64_t n, int
 
 void launch_quantize_rows(const float* w, int64_t rows, int64_t cols, int8_t* q, float* scales, hipStream_t st);
 
+// Persistent batch-1 decode step (decode_step.hip): every layer and the LM head in one
+// launch of one workgroup per CU, stages separated by grid barriers. All layer projections
+// must be int8; the LM head may be int8 or f32.
+struct StepLayer {
+  const int8_t* qkv;  // [qkv_rows][ld_h]: q, k, v rows
+  const float* qkv_s;
+  const int8_t* o;  // [hidden][ld_h]
+  const float* o_s;
+  const int8_t* gu;  // [2*inter][ld_h]: gate/up rows interleaved
+  const float* gu_s;
+  const int8_t* down;  // [hidden][ld_i]
+  const float* down_s;
+  const float* attn_norm;
+  const float* ffn_norm;
+};
+struct StepParams {
+  int layers, hidden, heads, hkv, inter, vocab, qkv_rows;
+  int64_t ld_h, ld_i, ld_lm;  // weight row strides in elements
+  float eps, scale;
+  const StepLayer* L;  // device array [layers]
+  const void* lm;      // int8 or f32 [vocab][ld_lm]
+  const float* lm_s;
+  const float* final_norm;
+  const uint16_t* embed;
+  float* kv;
+  int num_blocks, block_size;
+  const float* rope_cos;
+  const float* rope_sin;
+  const int32_t* token;          // [1]
+  const pia_attn_entry* entry;   // [1]
+  const int32_t* tables;
+  float* x;        // [hidden] residual stream
+  float* qkv_buf;  // [qkv_rows]
+  float* attn;     // [hidden]
+  float* h;        // [inter]
+  float* part;     // [heads][max_splits][hd + 2]
+  float* logits;   // [vocab]
+  unsigned long long* amax;  // [kArgmaxSlots]
+  unsigned* flags;           // [num_cus * 32]
+  unsigned* attn_cnt;        // [hkv * 32] finished splits per kv head (zero between steps)
+  unsigned* step_ctr;        // [1]
+  int* err;                  // [1]
+  int max_splits;            // token splits per kv head
+  unsigned long long* trace;  // optional [16 * layers + 2] stage timestamps (workgroup 0), or null
+};
+struct StepShape {
+  int64_t hidden, heads, hkv, hd, inter, vocab, qkv_rows;
+  int64_t max_splits, max_tokens;  // token splits per kv head; tokens per split
+  bool lm_i8;
+};
+constexpr size_t kMaxStepSmem = 96 * 1024;
+// nullptr when the step kernel handles this shape on a device with num_cus CUs, else why not.
+const char* decode_step_unsupported(const StepShape& s, int num_cus);
+size_t decode_step_smem(const StepShape& s);
+// Token splits per kv head for a grid of num_cus workgroups.
+int decode_step_splits(int num_cus, int64_t hkv);
+void launch_decode_step(const StepParams& p, const StepShape& s, int num_cus, hipStream_t st);
+
 void launch_copy_block(float* kv, const pia_kv_layout& layout, int64_t src, int64_t dst, hipStream_t st);
 
 }  // namespace pia

@@ -113,6 +113,8 @@ _SIGS = {
     "pia_model_decode": (I32, [P, P, P, P, P, P, I64, P, P]),
     "pia_model_prefill": (I32, [P, P, I64, I64, P, I64, P, P]),
     "pia_model_profile": (I32, [P, I32]),
+    "pia_model_set_decode_path": (I32, [P, I32]),
+    "pia_model_decode_path_used": (I32, [P]),
     "pia_model_profile_get": (I32, [P, P, P, P, I32]),
     "pia_model_bench_class": (I32, [P, I32, I64, I32, C.POINTER(C.c_double), C.POINTER(I64)]),
     "pia_bench_projection": (I32, [P, I64, I64, I64, I32, I32, C.POINTER(C.c_double), C.POINTER(I64)]),
@@ -497,7 +499,15 @@ class Model:
     def profile(self, on: bool):
         check(lib().pia_model_profile(self.h, int(on)))
 
-    PROFILE_CLASSES = ("qkv", "o", "gate_up", "down", "lm_head", "attention", "other")
+    PROFILE_CLASSES = ("qkv", "o", "gate_up", "down", "lm_head", "attention", "other", "step")
+
+    def set_decode_path(self, path: int):
+        """0: per-kernel launches (default); 1: persistent batch-1 decode step when supported."""
+        check(lib().pia_model_set_decode_path(self.h, path))
+
+    def decode_path_used(self) -> int:
+        """Path of the last decode: 0 per-kernel launches, 1 persistent step."""
+        return int(lib().pia_model_decode_path_used(self.h))
 
     def profile_get(self):
         """(ms, algorithmic bytes, launches) per class of the last profiled call."""

@@ -22,13 +22,16 @@ def _rel(a, b):
     return float(np.max(np.abs(a - b)) / max(1e-30, np.max(np.abs(b))))
 
 
-def greedy_session(ctx, cfg, weights, prompt, steps, block_size=16):
+def greedy_session(ctx, cfg, weights, prompt, steps, block_size=16, path=0, expect_path=None):
     """Prefill `prompt`, then `steps` greedy decode steps at batch 1, independently on the GPU
-    and on the oracle (each side feeds back its own argmax)."""
+    and on the oracle (each side feeds back its own argmax). `path` selects the GPU decode path
+    (0: per-kernel launches, 1: persistent single-launch step where supported); every decode
+    must have run on `expect_path` when given."""
     n_tok = len(prompt) + steps
     nb = (n_tok + block_size - 1) // block_size
     table = list(range(nb))  # a fresh FIFO pool hands out 0..nb-1
     gm = pia.Model(ctx, cfg, weights)
+    gm.set_decode_path(path)
     gm.kv_alloc(nb + 1, block_size)
     om_ = orc.OracleModel(cfg, weights)
     kv = np.zeros(orc.kv_floats(cfg, nb + 1, block_size), np.float32)
@@ -40,6 +43,8 @@ def greedy_session(ctx, cfg, weights, prompt, steps, block_size=16):
     for i in range(steps - 1):
         pos = len(prompt) + i
         lg, am = gm.decode([gtoks[-1]], [pos], [table])
+        if expect_path is not None:
+            assert gm.decode_path_used() == expect_path
         lc = om_.decode([ctoks[-1]], [pos], [table], kv, nb + 1, block_size)
         if gtoks == ctoks:
             rels.append(_rel(lg[0], lc[0]))
@@ -69,14 +74,15 @@ def test_golden_fixture_f32_on_gpu(ctx):
     assert np.max(np.abs(split - lg)) < 1e-5
 
 
-def test_config1_tiny_int8_greedy_parity(ctx):
+@pytest.mark.parametrize("path", [0, 1], ids=["per_kernel", "persistent"])
+def test_config1_tiny_int8_greedy_parity(ctx, path):
     """dim 128, 2 layers, 4/2 heads, FFN 344, vocab 512, block 16, 48-token
-    prompt, 40 greedy steps, int8 projections incl. lm_head."""
+    prompt, 40 greedy steps, int8 projections incl. lm_head; on both decode paths."""
     cfg = pia.TINY_C1
     w = pia.synth_weights(cfg, seed=1)
     prompt = np.random.default_rng(1).integers(0, cfg.vocab, 48).tolist()
-    g, c, rel = greedy_session(ctx, cfg, w, prompt, 40)
-    print(f"config1: rel max|dlogit|={rel:.3g} tokens={g[:10]}...")
+    g, c, rel = greedy_session(ctx, cfg, w, prompt, 40, path=path, expect_path=path)
+    print(f"config1 path {path}: rel max|dlogit|={rel:.3g} tokens={g[:10]}...")
     assert g == c
     assert rel <= LOGIT_TOL
 
@@ -86,15 +92,56 @@ def test_config1_f32_lm_head_variant(ctx):
     cfg = pia.TINY_C1
     w = pia.synth_weights(cfg, seed=2, lm_head_int8=False)
     prompt = np.random.default_rng(2).integers(0, cfg.vocab, 48).tolist()
-    g, c, rel = greedy_session(ctx, cfg, w, prompt, 40)
+    # An f32 LM head keeps batch-1 decode on the per-kernel path even when the persistent
+    # step is requested.
+    g, c, rel = greedy_session(ctx, cfg, w, prompt, 40, path=1, expect_path=0)
     assert g == c and rel <= LOGIT_TOL
 
 
-def test_sliding_window_model(ctx):
+@pytest.mark.parametrize("path", [0, 1], ids=["per_kernel", "persistent"])
+def test_sliding_window_model(ctx, path):
     cfg = pia.LlamaConfig(hidden=128, layers=2, heads=4, kv_heads=2, inter=344, vocab=512, attention_window=20)
     w = pia.synth_weights(cfg, seed=3)
     prompt = np.random.default_rng(3).integers(0, cfg.vocab, 37).tolist()
-    g, c, rel = greedy_session(ctx, cfg, w, prompt, 12)
+    g, c, rel = greedy_session(ctx, cfg, w, prompt, 12, path=path, expect_path=path)
+    assert g == c and rel <= LOGIT_TOL
+
+
+def test_persistent_step_unmapped_tail(ctx):
+    """Batch-1 decode whose block table stops short of the position: the unmapped logical
+    block scores -inf and this step's K/V write is skipped (src/attention.rs:233-240,
+    src/model.rs:868-878), on the persistent step and on the oracle."""
+    cfg = pia.TINY_C1
+    w = pia.synth_weights(cfg, seed=5)
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab, 40).tolist()
+    gm = pia.Model(ctx, cfg, w)
+    gm.set_decode_path(1)
+    gm.kv_alloc(4, 16)
+    om_ = orc.OracleModel(cfg, w)
+    kv = np.zeros(orc.kv_floats(cfg, 4, 16), np.float32)
+    gm.prefill(prompt, 0, [0, 1, 2])
+    om_.prefill(prompt, 0, [0, 1, 2], kv, 4, 16)
+    tok = 7
+    for pos in range(40, 46):
+        lg, am = gm.decode([tok], [pos], [[0, 1]])
+        assert gm.decode_path_used() == 1
+        lc = om_.decode([tok], [pos], [[0, 1]], kv, 4, 16)
+        assert _rel(lg[0], lc[0]) <= LOGIT_TOL
+        assert int(am[0]) == orc.argmax(lc[0])
+        tok = int(am[0])
+
+
+def test_persistent_step_llama3_shape(ctx):
+    """The persistent step at Llama-3-8B layer shapes (hidden 4096, 32/8 heads, head_dim 128,
+    FFN 14336, rotary theta 500000), two layers and a 16k vocabulary to keep the oracle fast:
+    300-token prompt (several token splits per kv head), 12 greedy steps."""
+    cfg = pia.LlamaConfig(hidden=4096, layers=2, heads=32, kv_heads=8, inter=14336, vocab=16384,
+                          rope_theta=500000.0)
+    print("[llama3-shape] building weights", flush=True)
+    w = pia.synth_weights(cfg, seed=11)
+    prompt = np.random.default_rng(11).integers(0, cfg.vocab, 300).tolist()
+    g, c, rel = greedy_session(ctx, cfg, w, prompt, 12, path=1, expect_path=1)
+    print(f"llama3-shape: rel max|dlogit|={rel:.3g}")
     assert g == c and rel <= LOGIT_TOL
 
 
@@ -107,7 +154,11 @@ def test_config2_tinyllama_b1_greedy_parity(ctx):
     w = pia.synth_weights(cfg, seed=2024)
     prompt = np.random.default_rng(2024).integers(0, cfg.vocab, 512).tolist()
     print("[config2] running GPU + oracle sessions", flush=True)
-    g, c, rel = greedy_session(ctx, cfg, w, prompt, 256)
+    g, c, rel = greedy_session(ctx, cfg, w, prompt, 256, expect_path=0)
+    assert g == c
+    # The same session on the persistent single-launch step.
+    g, c, rel1 = greedy_session(ctx, cfg, w, prompt, 256, path=1, expect_path=1)
+    rel = max(rel, rel1)
     print(f"config2: rel max|dlogit|={rel:.3g} first tokens {g[:8]}")
     assert g == c
     assert rel <= LOGIT_TOL
