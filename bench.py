@@ -30,7 +30,7 @@ import pia  # noqa: E402
 METRIC = "int8 decode tok/s (B=1,32) + int8 GEMV HBM GB/s as % of ~8 TB/s peak"
 # HBM bytes per launch of the gate/up projection at batch 1, from rocprofv3 FETCH_SIZE and
 # WRITE_SIZE runs scaled by a 256 MiB copy (profiles/decode_b1_projection_traffic.md).
-TRAFFIC_GATE_UP_B1 = 23_420_000
+TRAFFIC_GATE_UP_B1 = 23_450_000
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix-core peak, TOP/s
 SEED = 2024

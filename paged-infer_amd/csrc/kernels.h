@@ -11,9 +11,9 @@
 
 namespace pia {
 
-// Slots per batch row of the fused argmax: spreading the atomics over 64 addresses keeps
+// Slots per batch row of the fused argmax: spreading the atomics over 256 addresses keeps
 // thousands of workgroups from serializing on one.
-constexpr int kArgmaxSlots = 64;
+constexpr int kArgmaxSlots = 256;
 
 // Epilogue of a projection: store, accumulate into the destination (residual add, as
 // src/model.rs:1127-1129 and :1165-1167 do with proj_out / ff_down), or SwiGLU over

@@ -86,6 +86,7 @@ __device__ inline float wave_sum(float v) {
 }
 
 constexpr int kWaves = 4;  // wavefronts per workgroup
+constexpr int64_t kMaxStagedCols = 16384;  // batch-1 vectors up to this length are staged in LDS
 constexpr int kMaxNormBatch = 64;
 
 enum { kEpiStore = 0, kEpiAdd = 1, kEpiSwiglu = 2 };
@@ -269,6 +270,214 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv(const TW* __restrict__ W, 
   }
 }
 
+// Batch-1 int8 projection with the activation vector staged once per workgroup in LDS.
+// The vector's loads (and the norm weights') are issued before the weight loads, so the
+// RMSNorm reduction runs while the weights are in flight; the main loop then reads the
+// normalized vector from LDS instead of L2. LDS layout: column c at c + 4 * (c / 64), which
+// makes each lane's 16 consecutive floats start on a distinct group of banks.
+constexpr int kXPre = 8;  // float4 of the vector per thread loaded before the weights
+__device__ inline int xs_index(int c) { return c + ((c >> 6) << 2); }
+
+template <int R, int UNR, int EPI, bool NORM, bool AMAX>
+__global__ __launch_bounds__(64 * kWaves) void k_gemv1(const int8_t* __restrict__ W, int64_t ldw,
+                                                       const float* __restrict__ S, const float* __restrict__ X,
+                                                       const float* __restrict__ NW, float eps, float* __restrict__ O,
+                                                       int64_t osr, int rows, int cols,
+                                                       unsigned long long* __restrict__ amax) {
+  extern __shared__ float xs[];
+  __shared__ float red[kWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * kWaves + wave) * R;
+  constexpr int kStep = 64 * 16 * UNR;
+  const int n4 = cols >> 2;                              // cols % 4 == 0 on this path
+  const int kpad = (cols + 1023) / 1024 * 1024;          // zero padded to whole 1024-column chunks
+  const float4* X4 = reinterpret_cast<const float4*>(X);
+  const float4* NW4 = reinterpret_cast<const float4*>(NW);
+
+  // 1. The vector (and norm weights): the first kXPre float4 per thread.
+  float4 xv[kXPre], wv[kXPre];
+#pragma unroll
+  for (int u = 0; u < kXPre; ++u) {
+    const int i = threadIdx.x + u * 64 * kWaves;
+    xv[u] = i < n4 ? X4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (NORM) wv[u] = i < n4 ? NW4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  // 2. The first batch of weights.
+  const int8_t* wrow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) wrow[r] = W + static_cast<int64_t>(min(row0 + r, rows - 1)) * ldw;
+  Raw<int8_t, 16> raw[UNR][R];
+  auto load_batch = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int c = base + (u * 64 + lane) * 16;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (c < cols) raw[u][r].load(wrow[r] + c);
+        else raw[u][r].zero();
+      }
+    }
+  };
+  load_batch(0);
+  // 3. Vector into LDS (the rest of a long vector now), sum of squares, zero padding.
+  float ss = 0.0f;
+  auto put4 = [&](int i, float4 v) {
+    float* d = xs + xs_index(4 * i);
+    d[0] = v.x, d[1] = v.y, d[2] = v.z, d[3] = v.w;
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  };
+#pragma unroll
+  for (int u = 0; u < kXPre; ++u) {
+    const int i = threadIdx.x + u * 64 * kWaves;
+    if (i < n4) put4(i, xv[u]);
+  }
+  for (int i = threadIdx.x + kXPre * 64 * kWaves; i < n4; i += 64 * kWaves) put4(i, X4[i]);
+  for (int c = cols + threadIdx.x; c < kpad; c += 64 * kWaves) xs[xs_index(c)] = 0.0f;
+  if constexpr (NORM) {
+    // RMSNorm (src/math.rs:4-22): x * (1/rms) * w, in that order.
+    ss = wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) t += red[w];
+    const float inv = 1.0f / sqrtf(t / static_cast<float>(cols) + eps);
+    auto norm4 = [&](int i, float4 v, float4 w) {
+      float* d = xs + xs_index(4 * i);
+      d[0] = (v.x * inv) * w.x, d[1] = (v.y * inv) * w.y, d[2] = (v.z * inv) * w.z, d[3] = (v.w * inv) * w.w;
+    };
+#pragma unroll
+    for (int u = 0; u < kXPre; ++u) {
+      const int i = threadIdx.x + u * 64 * kWaves;
+      if (i < n4) norm4(i, xv[u], wv[u]);
+    }
+    for (int i = threadIdx.x + kXPre * 64 * kWaves; i < n4; i += 64 * kWaves) {
+      const float* d = xs + xs_index(4 * i);
+      norm4(i, make_float4(d[0], d[1], d[2], d[3]), NW4[i]);
+    }
+  }
+  __syncthreads();
+  // Waves past the last row skip the work but stay for the workgroup's argmax reduction.
+  const bool active = row0 < rows;
+
+  // 4. Stream the rows against the staged vector.
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+  for (int base = 0; active && base < cols; base += kStep) {
+    if (base != 0) load_batch(base);
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int c = base + (u * 64 + lane) * 16;
+      if (c < cols) {
+        float x16[16];
+        const float4* xp = reinterpret_cast<const float4*>(xs + xs_index(c));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 v = xp[q];
+          x16[4 * q] = v.x, x16[4 * q + 1] = v.y, x16[4 * q + 2] = v.z, x16[4 * q + 3] = v.w;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float w[16];
+          raw[u][r].widen(w);
+#pragma unroll
+          for (int j = 0; j < 16; ++j) acc[r] = __builtin_fmaf(w[j], x16[j], acc[r]);
+        }
+      }
+    }
+  }
+  float mine = 0.0f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float s = wave_sum(acc[r]);
+    if (lane == r) mine = s;
+  }
+  const int row = row0 + lane;
+  if constexpr (EPI == kEpiSwiglu) {
+    // Lanes r and r + 1 hold the gate and up results of output row (row0 + r) / 2.
+    const float up = __shfl_down(mine, 1, 64);
+    if (active && lane < R && (lane & 1) == 0 && row + 1 < rows) {
+      const float g = mine * S[row];
+      const float u = up * S[row + 1];
+      const float silu = g / (1.0f + expf(-g));
+      O[static_cast<int64_t>(row >> 1) * osr] = silu * u;
+    }
+  } else {
+    const bool valid = active && lane < R && row < rows;
+    float v = 0.0f;
+    if (valid) {
+      v = mine * S[row];
+      float* o = O + static_cast<int64_t>(row) * osr;
+      if (EPI == kEpiAdd) *o = *o + v;
+      else *o = v;
+    }
+    if constexpr (AMAX) {
+      // Greedy argmax: max of (order key, row) over the workgroup's rows, then one atomic per
+      // workgroup into one of the slots.
+      __shared__ unsigned long long wbest[kWaves];
+      unsigned long long cand = valid ? (static_cast<unsigned long long>(order_key(v)) << 32) | static_cast<uint32_t>(row) : 0ull;
+      cand = wave_max_u64(cand);
+      if (lane == 0) wbest[wave] = cand;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        unsigned long long m = wbest[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) m = wbest[w] > m ? wbest[w] : m;
+        if (m) atomicMax(&amax[blockIdx.x & (kArgmaxSlots - 1)], m);
+      }
+    }
+  }
+}
+
+template <int R, int UNR, int EPI>
+void go1(const GemvArgs& g, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((g.rows + kWaves * R - 1) / (kWaves * R)));
+  const int kpad = static_cast<int>((g.cols + 1023) / 1024 * 1024);
+  const size_t smem = static_cast<size_t>(kpad + kpad / 16) * 4;
+  const auto* w = static_cast<const int8_t*>(g.W);
+#define PIA_GEMV1(NORM, AMAX)                                                                                \
+  do {                                                                                                       \
+    static bool raised = false;                                                                              \
+    if (!raised && smem > 65536) {                                                                           \
+      PIA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv1<R, UNR, EPI, NORM, AMAX>),           \
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,                                \
+                                  static_cast<int>((kMaxStagedCols + kMaxStagedCols / 16) * 4)));            \
+      raised = true;                                                                                         \
+    }                                                                                                        \
+    hipLaunchKernelGGL((k_gemv1<R, UNR, EPI, NORM, AMAX>), grid, dim3(64 * kWaves), smem, st, w, g.ldw,      \
+                       g.scales, g.x, g.norm_w, g.eps, g.out, g.osr, static_cast<int>(g.rows),               \
+                       static_cast<int>(g.cols), g.amax);                                                    \
+  } while (0)
+  if constexpr (EPI == kEpiStore) {
+    if (g.amax) {
+      if (g.norm_w) PIA_GEMV1(true, true);
+      else PIA_GEMV1(false, true);
+      return;
+    }
+  }
+  if (g.norm_w) PIA_GEMV1(true, false);
+  else PIA_GEMV1(false, false);
+#undef PIA_GEMV1
+}
+
+template <int R, int UNR>
+void go1_epi(const GemvArgs& g, hipStream_t st) {
+  if (g.epi == Epi::Add) go1<R, UNR, kEpiAdd>(g, st);
+  else if (g.epi == Epi::Swiglu) go1<R, UNR, kEpiSwiglu>(g, st);
+  else go1<R, UNR, kEpiStore>(g, st);
+}
+
+template <int R>
+void go1_unr(const GemvArgs& g, hipStream_t st) {
+  const int64_t chunks = (g.cols / 16 + 63) / 64;
+  if (chunks <= 1) go1_epi<R, 1>(g, st);
+  else if (chunks <= 2) go1_epi<R, 2>(g, st);
+  else if (chunks <= 4) go1_epi<R, 4>(g, st);
+  else if (chunks <= 6) go1_epi<R, 6>(g, st);
+  else go1_epi<R, 8>(g, st);
+}
+
 struct Launch {
   const void* W;
   int64_t ldw;
@@ -352,6 +561,14 @@ void launch_gemv(const GemvArgs& g, hipStream_t st) {
            static_cast<int>(g.rows), static_cast<int>(g.cols), static_cast<int>(g.batch), g.amax, st};
   const bool xv16 = g.ldx % 16 == 0 && aligned(g.x, 64) && (!g.norm_w || aligned(g.norm_w, 64));
   const bool xv4 = g.ldx % 4 == 0 && aligned(g.x, 16) && (!g.norm_w || aligned(g.norm_w, 16));
+  if (g.wkind == 1 && g.batch == 1 && g.cols % 16 == 0 && g.ldw % 16 == 0 && aligned(g.W, 16) && aligned(g.x, 16) &&
+      (!g.norm_w || aligned(g.norm_w, 16)) && g.cols <= kMaxStagedCols) {
+    PIA_REQUIRE(g.scales != nullptr, "gemv: int8 weights need scales");
+    if (g.rows >= 4 * kWaves * 512) go1_unr<4>(g, st);
+    else go1_unr<2>(g, st);
+    PIA_HIP(hipGetLastError());
+    return;
+  }
   if (g.wkind == 1) {
     PIA_REQUIRE(g.scales != nullptr, "gemv: int8 weights need scales");
     if (g.ldw % 16 == 0 && aligned(g.W, 16) && xv16) by_r<int8_t, 16>(a, g.epi);
