@@ -21,6 +21,8 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
+// Whole 64-entry chunks from which the LDS-tiled kernel takes over (prefill sizes).
+constexpr int64_t kTileMinChunks = 4;
 
 __device__ inline float block_reduce_sum(float v, float* red) {
 #pragma unroll
@@ -418,6 +420,156 @@ void go_dec(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int k
                        osb, osr, rows, batch, amax);
 }
 
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// Prefill GEMM (many batch entries): one workgroup per 128 weight rows x 192 digit columns
+// (64 batch entries). Both operand tiles go through LDS in 64-byte K stages, double buffered:
+// the next stage's global loads are in registers while the current stage's MFMAs run. Four
+// waves, each 64 rows x 96 columns = 2 x 3 tiles of v_mfma_i32_32x32x32_i8.
+namespace tile {
+constexpr int kBM = 128, kBN = 192, kBK = 64;
+constexpr int kPitch = kBK + 16;  // LDS row pitch in bytes (staggers rows across banks)
+constexpr int kStage = (kBM + kBN) * kPitch;
+constexpr int kWLoads = kBM * kBK / 16 / kThreads;  // 16-byte loads per thread per stage: 2
+constexpr int kDLoads = kBN * kBK / 16 / kThreads;  // 3
+constexpr size_t kSmem = 2 * kStage > 64 * kBN * 4 ? 2 * kStage : 64 * kBN * 4;
+}  // namespace tile
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads) void k_gemm_tile(const int8_t* __restrict__ W, int64_t ldw,
+                                                        const float* __restrict__ S, const int8_t* __restrict__ D,
+                                                        int kpad, const float* __restrict__ pow2,
+                                                        float* __restrict__ O, int64_t osb, int64_t osr, int rows) {
+  using namespace tile;
+  extern __shared__ int8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row0 = blockIdx.x * kBM;
+  const int col0 = blockIdx.y * kBN;  // digit rows of D; batch entries 64 * blockIdx.y ..
+  const int wr = wave & 1, wc = wave >> 1;
+  const int r_l = lane & 31, kh = lane >> 5;
+
+  // Global -> register staging of one K stage: thread t covers 16-byte segment (t % 4) of
+  // rows t / 4, t / 4 + 64, ... of each tile.
+  const int seg = tid & 3, trow = tid >> 2;
+  const int8_t* wsrc[kWLoads];
+  const int8_t* dsrc[kDLoads];
+#pragma unroll
+  for (int u = 0; u < kWLoads; ++u)
+    wsrc[u] = W + static_cast<int64_t>(min(row0 + trow + 64 * u, rows - 1)) * ldw + seg * 16;
+#pragma unroll
+  for (int u = 0; u < kDLoads; ++u) dsrc[u] = D + static_cast<int64_t>(col0 + trow + 64 * u) * kpad + seg * 16;
+  v4i wreg[kWLoads], dreg[kDLoads];
+  auto gload = [&](int kt) {
+    const int64_t off = static_cast<int64_t>(kt) * kBK;
+#pragma unroll
+    for (int u = 0; u < kWLoads; ++u) wreg[u] = *reinterpret_cast<const v4i*>(wsrc[u] + off);
+#pragma unroll
+    for (int u = 0; u < kDLoads; ++u) dreg[u] = *reinterpret_cast<const v4i*>(dsrc[u] + off);
+  };
+  auto sstore = [&](int buf) {
+    int8_t* ws = lds + buf * kStage;
+    int8_t* ds = ws + kBM * kPitch;
+#pragma unroll
+    for (int u = 0; u < kWLoads; ++u) *reinterpret_cast<v4i*>(ws + (trow + 64 * u) * kPitch + seg * 16) = wreg[u];
+#pragma unroll
+    for (int u = 0; u < kDLoads; ++u) *reinterpret_cast<v4i*>(ds + (trow + 64 * u) * kPitch + seg * 16) = dreg[u];
+  };
+
+  v16i acc[2][3];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+
+  const int nk = kpad / kBK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const bool more = kt + 1 < nk;
+    if (more) gload(kt + 1);
+    const int8_t* ws = lds + (kt & 1) * kStage;
+    const int8_t* ds = ws + kBM * kPitch;
+#pragma unroll
+    for (int kk = 0; kk < kBK; kk += 32) {
+      v4i a[2], b[3];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        a[i] = *reinterpret_cast<const v4i*>(ws + (wr * 64 + i * 32 + r_l) * kPitch + kk + kh * 16);
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+        b[j] = *reinterpret_cast<const v4i*>(ds + (wc * 96 + j * 32 + r_l) * kPitch + kk + kh * 16);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    // Buffer (kt + 1) & 1 was last read in iteration kt - 1, before that iteration's barrier.
+    if (more) sstore((kt + 1) & 1);
+    __syncthreads();
+  }
+
+  // Epilogue, 64 weight rows at a time: the C tile half goes to LDS ([64][kBN] int32), then
+  // thread -> (row, batch entry) recombines the entry's three digit columns. 32x32 result
+  // layout: lane holds column lane % 32 and, in register v, row 8 * (v / 4) + 4 * (lane / 32)
+  // + v % 4.
+  int* ct = reinterpret_cast<int*>(lds);
+  for (int half = 0; half < 2; ++half) {
+    if (wr == half) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int r = i * 32 + 8 * (v >> 2) + 4 * kh + (v & 3);
+            ct[r * kBN + wc * 96 + j * 32 + r_l] = acc[i][j][v];
+          }
+    }
+    __syncthreads();
+    const int b0 = col0 / 3;  // first batch entry of the tile
+    for (int idx = tid; idx < 64 * (kBN / 3); idx += kThreads) {
+      const int r = idx / (kBN / 3), b = idx % (kBN / 3);
+      const int row = row0 + half * 64 + r;
+      const int* cr = ct + r * kBN + 3 * b;
+      const int64_t sum = static_cast<int64_t>(cr[0]) + 256 * static_cast<int64_t>(cr[1]) + 65536 * static_cast<int64_t>(cr[2]);
+      const float y = static_cast<float>(sum) * pow2[b0 + b];
+      if constexpr (EPI == kEpiSwiglu) {
+        if ((r & 1) == 0 && row + 1 < rows) {
+          const int* cu = cr + kBN;
+          const int64_t su = static_cast<int64_t>(cu[0]) + 256 * static_cast<int64_t>(cu[1]) + 65536 * static_cast<int64_t>(cu[2]);
+          const float yu = static_cast<float>(su) * pow2[b0 + b];
+          const float g = y * S[row];
+          const float u = yu * S[row + 1];
+          const float silu = g / (1.0f + expf(-g));
+          O[static_cast<int64_t>(b0 + b) * osb + static_cast<int64_t>(row >> 1) * osr] = silu * u;
+        }
+      } else if (row < rows) {
+        const float v = y * S[row];
+        float* o = O + static_cast<int64_t>(b0 + b) * osb + static_cast<int64_t>(row) * osr;
+        if (EPI == kEpiAdd) *o = *o + v;
+        else *o = v;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int EPI>
+void go_tile(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, const float* pow2, float* O,
+             int64_t osb, int64_t osr, int rows, int tiles_n, hipStream_t st) {
+  static bool raised = false;
+  if (!raised && tile::kSmem > 65536) {
+    PIA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_tile<EPI>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(tile::kSmem)));
+    raised = true;
+  }
+  hipLaunchKernelGGL((k_gemm_tile<EPI>), dim3((rows + tile::kBM - 1) / tile::kBM, tiles_n), dim3(kThreads), tile::kSmem,
+                     st, W, ldw, S, D, kpad, pow2, O, osb, osr, rows);
+}
+
 }  // namespace
 
 int64_t digit_cols(int64_t batch) { return (3 * batch + 15) / 16 * 16; }
@@ -476,7 +628,14 @@ void launch_gemm_i8_mfma(const int8_t* W, int64_t ldw, const float* scales, cons
       default: fail(PIA_ERR_INVALID, "gemm: bad column tile");
     }
   };
-  if (full) launch(0, full, 64);
+  if (full >= kTileMinChunks && !amax) {
+    // Many batch entries (prefill): the LDS-tiled kernel over the whole 64-entry chunks.
+    if (epi == Epi::Add) go_tile<kEpiAdd>(W, ldw, scales, dig, k, pow2, out, osb, osr, r, static_cast<int>(full), st);
+    else if (epi == Epi::Swiglu) go_tile<kEpiSwiglu>(W, ldw, scales, dig, k, pow2, out, osb, osr, r, static_cast<int>(full), st);
+    else go_tile<kEpiStore>(W, ldw, scales, dig, k, pow2, out, osb, osr, r, static_cast<int>(full), st);
+  } else if (full) {
+    launch(0, full, 64);
+  }
   if (batch % 64) launch(full * 64, 1, static_cast<int>(batch % 64));
   PIA_HIP(hipGetLastError());
 }
