@@ -131,6 +131,20 @@ def test_persistent_step_unmapped_tail(ctx):
         tok = int(am[0])
 
 
+def test_prefill_tiled_gemm_ragged_shapes(ctx):
+    """Prefill of 300 tokens (four whole 64-entry chunks for the LDS-tiled matrix-core GEMM plus
+    a 44-entry remainder) at config-1 shapes, whose projections are not whole 128-row tiles
+    (gate/up 688 rows, q/k/v 256, o/down 128) and whose K is not whole 64-byte stages
+    (down: 344 columns). Logits of the last position and the K/V written by the prefill are
+    checked through the following greedy decode steps."""
+    cfg = pia.TINY_C1
+    w = pia.synth_weights(cfg, seed=7)
+    prompt = np.random.default_rng(7).integers(0, cfg.vocab, 300).tolist()
+    g, c, rel = greedy_session(ctx, cfg, w, prompt, 8)
+    print(f"tiled prefill: rel max|dlogit|={rel:.3g}")
+    assert g == c and rel <= LOGIT_TOL
+
+
 def test_persistent_step_llama3_shape(ctx):
     """The persistent step at Llama-3-8B layer shapes (hidden 4096, 32/8 heads, head_dim 128,
     FFN 14336, rotary theta 500000), two layers and a 16k vocabulary to keep the oracle fast:
