@@ -55,5 +55,9 @@ struct PinnedBuffer {
 hipStream_t stream_of(pia_context* ctx, void* stream);
 void check_layout(const pia_kv_layout* L);
 void quantize_rows_host(const float* w, int64_t rows, int64_t cols, int8_t* q, float* scales);
+// Fill projection slot `which` of `layer` from device bf16 rows [rows][cols]: kind 1 quantizes
+// them on the device (bit-exact with the host quantizer), kind 0 widens them to f32.
+void model_set_proj_bf16_dev(pia_model* m, int64_t layer, int32_t which, int kind, const uint16_t* src, int64_t rows,
+                             int64_t cols);
 
 }  // namespace pia

@@ -524,24 +524,50 @@ int64_t total_rows(pia_model* m, const Proj* p) {
   return 0;
 }
 
-void set_proj(pia_model* m, int64_t layer, int32_t which, int kind, const void* data, const float* scales) {
-  PIA_REQUIRE(m && data, "null argument");
-  PIA_REQUIRE(kind == 0 || scales, "int8 projection needs scales");
+// The slot's projection group, (re)allocated for `kind`, with every replayable step dropped.
+Target prepare_slot(pia_model* m, int64_t layer, int32_t which, int kind) {
   Target t = target_of(m, layer, which);
   PIA_HIP(hipSetDevice(m->ctx->device));
+  PIA_HIP(hipStreamSynchronize(m->st()));
   if (t.p->kind != kind) {
     PIA_REQUIRE(t.p->filled == 0 || t.p->kind < 0,
                 "fused projection group mixes int8 and f32 slots; set every slot of the group with one kind");
     alloc_proj(*t.p, kind, total_rows(m, t.p), t.cols);
+    PIA_HIP(hipDeviceSynchronize());  // the zero fill of the row padding precedes later stream work
   }
-  PIA_HIP(hipStreamSynchronize(m->st()));
   m->drop_graphs();  // a re-allocated projection moves; the step kernel's pointer table too
   m->step_state = -1;
+  return t;
+}
+
+void set_proj(pia_model* m, int64_t layer, int32_t which, int kind, const void* data, const float* scales) {
+  PIA_REQUIRE(m && data, "null argument");
+  PIA_REQUIRE(kind == 0 || scales, "int8 projection needs scales");
+  Target t = prepare_slot(m, layer, which, kind);
   upload_rows(*t.p, t.r0, t.rows, t.row_step, data, scales);
   t.p->filled |= t.bit;
 }
 
 }  // namespace
+
+namespace pia {
+void model_set_proj_bf16_dev(pia_model* m, int64_t layer, int32_t which, int kind, const uint16_t* src, int64_t rows,
+                             int64_t cols) {
+  PIA_REQUIRE(m && src, "null argument");
+  PIA_REQUIRE(kind == 0 || kind == 1, "projection kind must be 0 (f32) or 1 (int8)");
+  const Target want = target_of(m, layer, which);
+  PIA_REQUIRE(rows == want.rows && cols == want.cols, "projection shape does not match the model config");
+  Target t = prepare_slot(m, layer, which, kind);
+  Proj& p = *t.p;
+  if (kind == 1)
+    launch_quantize_rows_bf16(src, t.rows, t.cols, p.w.as<int8_t>() + t.r0 * p.ld, p.ld, p.s.as<float>() + t.r0,
+                              t.row_step, m->st());
+  else
+    launch_widen_rows_bf16(src, t.rows, t.cols, p.w.as<float>() + t.r0 * p.ld, p.ld, t.row_step, m->st());
+  PIA_HIP(hipStreamSynchronize(m->st()));
+  p.filled |= t.bit;
+}
+}  // namespace pia
 
 extern "C" {
 
@@ -619,6 +645,13 @@ pia_status pia_model_set_proj_i8(pia_model* m, int64_t layer, int32_t which, con
 pia_status pia_model_set_proj_f32(pia_model* m, int64_t layer, int32_t which, const float* w) {
   PIA_API_BEGIN
   set_proj(m, layer, which, 0, w, nullptr);
+  PIA_API_END
+}
+
+pia_status pia_model_get_config(const pia_model* m, pia_model_config* out) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(m && out, "null argument");
+  *out = m->cfg;
   PIA_API_END
 }
 

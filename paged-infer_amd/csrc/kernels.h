@@ -114,6 +114,12 @@ void launch_swiglu(const float* gu, int64_t ldgu, float* h, int64_t ldh, int64_t
 void launch_argmax(const float* logits, int64_t ld, int32_t* out, int64_t n, int64_t vocab, hipStream_t st);
 
 void launch_quantize_rows(const float* w, int64_t rows, int64_t cols, int8_t* q, float* scales, hipStream_t st);
+// Checkpoint loading: bf16 rows [rows][cols] quantized (bit-exact with launch_quantize_rows of
+// the widened rows) or widened, source row r written to destination row r * row_step.
+void launch_quantize_rows_bf16(const uint16_t* w, int64_t rows, int64_t cols, int8_t* q, int64_t ldq, float* scales,
+                               int64_t row_step, hipStream_t st);
+void launch_widen_rows_bf16(const uint16_t* w, int64_t rows, int64_t cols, float* out, int64_t ldo, int64_t row_step,
+                            hipStream_t st);
 
 // Persistent batch-1 decode step (decode_step.hip): every layer and the LM head in one
 // launch of one workgroup per CU, stages separated by grid barriers. All layer projections

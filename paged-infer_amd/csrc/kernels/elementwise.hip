@@ -158,14 +158,23 @@ __global__ __launch_bounds__(kThreads) void k_argmax(const float* __restrict__ l
   }
 }
 
+// Source element of a weight row: f32 as is, or bf16 bits widened exactly (bits << 16, the
+// conversion of half::bf16::to_f32 that src/model.rs:455-460 applies at load).
+__device__ inline float widen(float v) { return v; }
+__device__ inline float widen(uint16_t v) { return __uint_as_float(static_cast<uint32_t>(v) << 16); }
+
 // src/math.rs:456-469 on the device. IEEE division and roundf (half away from zero) make it
-// bit-identical to the host quantizer; the row max is order independent.
-__global__ __launch_bounds__(kThreads) void k_quantize(const float* __restrict__ w, int64_t cols,
-                                                       int8_t* __restrict__ q, float* __restrict__ scales) {
+// bit-identical to the host quantizer; the row max is order independent. Source row r lands
+// at destination row r * row_step (pitch ldq, scale at scales[r * row_step]).
+template <typename Src>
+__global__ __launch_bounds__(kThreads) void k_quantize(const Src* __restrict__ w, int64_t cols,
+                                                       int8_t* __restrict__ q, int64_t ldq,
+                                                       float* __restrict__ scales, int64_t row_step) {
   __shared__ float red[kThreads / 64 + 1];
-  const float* row = w + static_cast<int64_t>(blockIdx.x) * cols;
+  const Src* row = w + static_cast<int64_t>(blockIdx.x) * cols;
+  const int64_t dst_row = static_cast<int64_t>(blockIdx.x) * row_step;
   float m = 0.0f;
-  for (int64_t i = threadIdx.x; i < cols; i += kThreads) m = fmaxf(m, fabsf(row[i]));
+  for (int64_t i = threadIdx.x; i < cols; i += kThreads) m = fmaxf(m, fabsf(widen(row[i])));
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -179,13 +188,22 @@ __global__ __launch_bounds__(kThreads) void k_quantize(const float* __restrict__
   __syncthreads();
   const float max_abs = red[kThreads / 64];
   const float scale = max_abs > 0.0f ? max_abs / 127.0f : 1.0f;
-  if (threadIdx.x == 0) scales[blockIdx.x] = scale;
-  int8_t* qrow = q + static_cast<int64_t>(blockIdx.x) * cols;
+  if (threadIdx.x == 0) scales[dst_row] = scale;
+  int8_t* qrow = q + dst_row * ldq;
   for (int64_t i = threadIdx.x; i < cols; i += kThreads) {
-    float v = roundf(row[i] / scale);
+    float v = roundf(widen(row[i]) / scale);
     v = fminf(fmaxf(v, -127.0f), 127.0f);
     qrow[i] = static_cast<int8_t>(v);
   }
+}
+
+// PackedLinear::from_tensor (src/model.rs:140-163): bf16 rows widened to f32, row r at
+// destination row r * row_step (pitch ldo).
+__global__ __launch_bounds__(kThreads) void k_widen_rows(const uint16_t* __restrict__ w, int64_t cols,
+                                                         float* __restrict__ out, int64_t ldo, int64_t row_step) {
+  const uint16_t* row = w + static_cast<int64_t>(blockIdx.x) * cols;
+  float* orow = out + static_cast<int64_t>(blockIdx.x) * row_step * ldo;
+  for (int64_t i = threadIdx.x; i < cols; i += kThreads) orow[i] = widen(row[i]);
 }
 
 // KvLayout::copy_block: blockIdx.y = layer.
@@ -246,7 +264,28 @@ void launch_argmax(const float* logits, int64_t ld, int32_t* out, int64_t n, int
 void launch_quantize_rows(const float* w, int64_t rows, int64_t cols, int8_t* q, float* scales, hipStream_t st) {
   if (rows == 0) return;
   PIA_REQUIRE(rows < (int64_t(1) << 31), "quantize: too many rows");
-  hipLaunchKernelGGL(k_quantize, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, st, w, cols, q, scales);
+  hipLaunchKernelGGL(k_quantize<float>, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, st, w, cols, q, cols,
+                     scales, int64_t(1));
+  PIA_HIP(hipGetLastError());
+}
+
+void launch_quantize_rows_bf16(const uint16_t* w, int64_t rows, int64_t cols, int8_t* q, int64_t ldq, float* scales,
+                               int64_t row_step, hipStream_t st) {
+  if (rows == 0) return;
+  PIA_REQUIRE(rows < (int64_t(1) << 31), "quantize: too many rows");
+  PIA_REQUIRE(ldq >= cols && row_step >= 1, "quantize: bad destination pitch");
+  hipLaunchKernelGGL(k_quantize<uint16_t>, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, st, w, cols, q, ldq,
+                     scales, row_step);
+  PIA_HIP(hipGetLastError());
+}
+
+void launch_widen_rows_bf16(const uint16_t* w, int64_t rows, int64_t cols, float* out, int64_t ldo, int64_t row_step,
+                            hipStream_t st) {
+  if (rows == 0) return;
+  PIA_REQUIRE(rows < (int64_t(1) << 31), "widen: too many rows");
+  PIA_REQUIRE(ldo >= cols && row_step >= 1, "widen: bad destination pitch");
+  hipLaunchKernelGGL(k_widen_rows, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, st, w, cols, out, ldo,
+                     row_step);
   PIA_HIP(hipGetLastError());
 }
 

@@ -77,3 +77,26 @@ def compare(actual: np.ndarray, expected: np.ndarray):
 
     mism = sum(pick(a) != pick(e) for a, e in zip(actual, expected))
     return max_abs, mism
+
+
+def write_safetensors(path: Path, tensors: dict, dtypes: dict | None = None, metadata: dict | None = None):
+    """Write a safetensors file: 8-byte LE header length, JSON header, raw little-endian data.
+    `tensors` maps names to uint16 bf16-bit arrays (dtype "BF16") unless `dtypes` names another
+    safetensors dtype for the entry (the array's bytes are written as they are)."""
+    dtypes = dtypes or {}
+    header = {"__metadata__": metadata or {"format": "pt"}}
+    blobs, off = [], 0
+    for name, arr in tensors.items():
+        arr = np.ascontiguousarray(arr)
+        raw = arr.tobytes()
+        header[name] = {"dtype": dtypes.get(name, "BF16"), "shape": list(arr.shape),
+                        "data_offsets": [off, off + len(raw)]}
+        blobs.append(raw)
+        off += len(raw)
+    hj = json.dumps(header).encode()
+    hj += b" " * (-len(hj) % 8)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(hj)))
+        f.write(hj)
+        for b in blobs:
+            f.write(b)
