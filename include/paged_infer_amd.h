@@ -203,6 +203,25 @@ pia_status pia_model_set_norm(pia_model* m, int64_t layer, int32_t which, const 
 pia_status pia_model_set_proj_i8(pia_model* m, int64_t layer, int32_t which, const int8_t* q, const float* scales);
 /* Projection::F32 from host f32 weights (PackedLinear, src/model.rs:140-163). */
 pia_status pia_model_set_proj_f32(pia_model* m, int64_t layer, int32_t which, const float* w);
+/* The config the model was created with. */
+pia_status pia_model_get_config(const pia_model* m, pia_model_config* out);
+
+/* LlamaConfig::from_hf_config (src/model.rs:57-95): the architecture from a HuggingFace
+ * config.json. Fields absent from the file (or not of the reference's JSON type: unsigned
+ * integers for sizes, numbers for rms_norm_eps / rope_theta) keep LlamaConfig::default()
+ * (TinyLlama-1.1B, src/model.rs:37-53); num_key_value_heads defaults to num_attention_heads;
+ * attention_window is -1 (None). A missing or malformed file is PIA_ERR_INVALID. */
+pia_status pia_hf_config_read(const char* path, pia_model_config* out);
+
+/* ModelLoader::load_weights (src/model.rs:388-447): every tensor of a bf16 HuggingFace Llama
+ * safetensors checkpoint into a model created with the checkpoint's config. quantization:
+ * 0 = Projection::F32 (bf16 widened), 1 = Projection::Int8 (quantize_rows_i8 on the device,
+ * bit-exact with pia_quantize_rows_i8 of the widened rows) for the seven projections of every
+ * layer. lm_head_int8: 0 keeps the LM head f32 as the reference's loader does; 1 quantizes it
+ * too. Without lm_head.weight the embedding matrix is used (tied weights). A missing tensor,
+ * a dtype other than BF16 or a shape the config does not imply is PIA_ERR_INVALID naming the
+ * tensor, reported before anything is uploaded. */
+pia_status pia_model_load_safetensors(pia_model* m, const char* path, int32_t quantization, int32_t lm_head_int8);
 /* Bytes of device projection weights (LlamaWeights::weight_bytes, src/model.rs:590-608). */
 int64_t pia_model_weight_bytes(const pia_model* m);
 
@@ -231,6 +250,37 @@ pia_status pia_model_prefill(pia_model* m, const uint32_t* tokens, int64_t n, in
  * 1 persistent, -1 none yet). No counterpart in the reference (it has no GPU int8 path). */
 pia_status pia_model_set_decode_path(pia_model* m, int32_t path);
 int32_t pia_model_decode_path_used(const pia_model* m);
+
+/* ------------------------------------------------------------------------------------ */
+/* Speculative verification (src/speculative.rs, src/engine.rs:595-761).                  */
+/* ------------------------------------------------------------------------------------ */
+/* PromptLookupDrafter::draft (src/speculative.rs:71-101): up to k tokens that followed the
+ * most recent earlier occurrence of the longest suffix of context[0..n) whose length is in
+ * [min_ngram, max_ngram] (the engine uses 2, 8). Writes *n_out <= k tokens to out. */
+pia_status pia_prompt_lookup_draft(const uint32_t* context, int64_t n, int64_t k, int64_t min_ngram,
+                                   int64_t max_ngram, uint32_t* out, int64_t* n_out);
+/* verify_greedy (src/speculative.rs:204-223): the leading drafts equal to the model's argmax
+ * are accepted; *corrected = model_argmax[*n_accepted]. n_argmax must be n_drafts + 1. */
+pia_status pia_verify_greedy(const uint32_t* drafts, int64_t n_drafts, const uint32_t* model_argmax,
+                             int64_t n_argmax, int64_t* n_accepted, uint32_t* corrected);
+
+typedef struct pia_spec_group { /* SpecGroup (src/engine.rs:175-182) */
+  int64_t pos;        /* position of the held token; token j sits at pos + j */
+  int64_t n_tokens;   /* 1 (the held token) + number of drafts */
+  int64_t tokens_off; /* tokens[tokens_off .. + n_tokens): held token, then the drafts */
+  int64_t table_off;  /* the sequence's block table: tables[table_off .. + table_len) */
+  int64_t table_len;
+} pia_spec_group;
+
+/* Engine::run_groups + commit's verification (src/engine.rs:702-783): every group's positions
+ * flattened into batched decode passes of at most `capacity` entries (0 = one pass), each
+ * position's greedy argmax written to predictions (flattened group order, sum of n_tokens),
+ * then verify_greedy per group into n_accepted[g] / corrected[g] (either may be NULL).
+ * *passes (may be NULL) = model passes run. Block tables must already cover every position
+ * and be writable there (ensure_writable), as the engine's plan_step guarantees. */
+pia_status pia_model_verify_groups(pia_model* m, const pia_spec_group* groups, int64_t n_groups,
+                                   const uint32_t* tokens, const int32_t* tables, int64_t capacity,
+                                   uint32_t* predictions, int64_t* n_accepted, uint32_t* corrected, int64_t* passes);
 
 /* Per-kernel timing of the last pia_model_decode / pia_model_prefill call (HIP events around
  * every launch on the context stream), accumulated per class: 0 = q/k/v projection, 1 = o,

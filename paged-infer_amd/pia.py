@@ -25,6 +25,7 @@ LIB_PATH = HERE / "libpaged_infer_amd.so"
 HEADER = ROOT / "include" / "paged_infer_amd.h"
 
 PIA_OK = 0
+PIA_ERR_INVALID, PIA_ERR_HIP, PIA_ERR_OOM, PIA_ERR_NO_DEVICE = 1, 2, 3, 4
 SLOTS = {"wq": 0, "wk": 1, "wv": 2, "wo": 3, "w1": 4, "w2": 5, "w3": 6, "lm_head": 7}
 NORM_ATTN, NORM_FFN, NORM_FINAL = 0, 1, 2
 
@@ -50,6 +51,11 @@ class KvmStats(C.Structure):
     _fields_ = [("hits", C.c_uint64), ("misses", C.c_uint64), ("inserts", C.c_uint64), ("evictions", C.c_uint64),
                 ("tokens_saved", C.c_uint64), ("cow_copies", C.c_uint64), ("available_blocks", C.c_int64),
                 ("total_blocks", C.c_int64), ("active_sequences", C.c_int64), ("cached_entries", C.c_int64)]
+
+
+class SpecGroup(C.Structure):
+    _fields_ = [("pos", C.c_int64), ("n_tokens", C.c_int64), ("tokens_off", C.c_int64), ("table_off", C.c_int64),
+                ("table_len", C.c_int64)]
 
 
 class ModelConfig(C.Structure):
@@ -108,6 +114,12 @@ _SIGS = {
     "pia_model_set_proj_i8": (I32, [P, I64, I32, P, P]),
     "pia_model_set_proj_f32": (I32, [P, I64, I32, P]),
     "pia_model_weight_bytes": (I64, [P]),
+    "pia_model_get_config": (I32, [P, C.POINTER(ModelConfig)]),
+    "pia_prompt_lookup_draft": (I32, [P, I64, I64, I64, I64, P, C.POINTER(I64)]),
+    "pia_verify_greedy": (I32, [P, I64, P, I64, C.POINTER(I64), C.POINTER(C.c_uint32)]),
+    "pia_model_verify_groups": (I32, [P, P, I64, P, P, I64, P, P, P, C.POINTER(I64)]),
+    "pia_hf_config_read": (I32, [C.c_char_p, C.POINTER(ModelConfig)]),
+    "pia_model_load_safetensors": (I32, [P, C.c_char_p, I32, I32]),
     "pia_model_kv_alloc": (I32, [P, I64, I64]),
     "pia_model_kv": (I32, [P, C.POINTER(P), C.POINTER(KvLayout)]),
     "pia_model_decode": (I32, [P, P, P, P, P, P, I64, P, P]),
@@ -167,6 +179,26 @@ def quantize_rows_i8(w: np.ndarray):
     s = np.empty(rows, np.float32)
     check(lib().pia_quantize_rows_i8(ptr(w), rows, cols, ptr(q), ptr(s)))
     return q, s
+
+
+def prompt_lookup_draft(context, k: int, min_ngram: int = 2, max_ngram: int = 8) -> list[int]:
+    """PromptLookupDrafter::draft (src/speculative.rs:71-101); the engine's drafter is (2, 8)."""
+    c = np.ascontiguousarray(np.asarray(context, np.uint32))
+    out = np.zeros(max(k, 1), np.uint32)
+    n = I64()
+    check(lib().pia_prompt_lookup_draft(ptr(c) if c.size else None, c.size, k, min_ngram, max_ngram, ptr(out),
+                                        C.byref(n)))
+    return [int(t) for t in out[:n.value]]
+
+
+def verify_greedy(drafts, model_argmax) -> tuple[list[int], int]:
+    """verify_greedy (src/speculative.rs:204-223): (accepted drafts, corrected token)."""
+    d = np.ascontiguousarray(np.asarray(drafts, np.uint32))
+    m = np.ascontiguousarray(np.asarray(model_argmax, np.uint32))
+    a, corr = I64(), C.c_uint32()
+    check(lib().pia_verify_greedy(ptr(d) if d.size else None, d.size, ptr(m) if m.size else None, m.size,
+                                  C.byref(a), C.byref(corr)))
+    return [int(t) for t in d[:a.value]], int(corr.value)
 
 
 def synth_normal(seed: int, stream: int, n: int, std: float = 0.02) -> np.ndarray:
@@ -389,6 +421,29 @@ class LlamaConfig:
     def head_dim(self):
         return self.hidden // self.heads
 
+    @classmethod
+    def from_hf_config(cls, path) -> "LlamaConfig":
+        """LlamaConfig::from_hf_config (src/model.rs:57-95): absent fields keep the TinyLlama
+        defaults; raises PiaError for a missing or malformed file."""
+        c = ModelConfig()
+        check(lib().pia_hf_config_read(str(path).encode(), C.byref(c)))
+        return cls._from_c(c)
+
+    @classmethod
+    def beside_checkpoint(cls, model_path) -> "LlamaConfig":
+        """LlamaConfig::beside_checkpoint (src/model.rs:97-102): config.json next to the
+        checkpoint, else the defaults."""
+        try:
+            return cls.from_hf_config(Path(model_path).with_name("config.json"))
+        except PiaError:
+            return cls(hidden=2048, layers=22, heads=32, kv_heads=4, inter=5632, vocab=32000)
+
+    @classmethod
+    def _from_c(cls, c: ModelConfig) -> "LlamaConfig":
+        return cls(hidden=c.hidden, layers=c.layers, heads=c.heads, kv_heads=c.kv_heads, inter=c.inter,
+                   vocab=c.vocab, rms_eps=c.rms_eps, rope_theta=c.rope_theta,
+                   attention_window=None if c.attention_window < 0 else c.attention_window)
+
     def c(self) -> ModelConfig:
         return ModelConfig(self.hidden, self.layers, self.heads, self.kv_heads, self.inter, self.vocab, self.rms_eps,
                            self.rope_theta, -1 if self.attention_window is None else self.attention_window)
@@ -400,13 +455,17 @@ class Model:
     attn_norm, ffn_norm and wq/wk/wv/wo/w1/w2/w3, each projection either a (q int8, scales f32)
     pair (Projection::Int8) or an f32 matrix (Projection::F32)."""
 
-    def __init__(self, ctx: Context, cfg: LlamaConfig, weights: dict):
+    def __init__(self, ctx: Context, cfg: LlamaConfig, weights: dict | None):
         self.ctx, self.cfg = ctx, cfg
         h = P()
         cc = cfg.c()
         check(lib().pia_model_create(ctx.h, C.byref(cc), C.byref(h)))
         self.h = h
         ctx._children.add(self)
+        self.kv_ptr = None
+        self.layout = None
+        if weights is None:
+            return
         L = lib()
         check(L.pia_model_set_embedding(h, ptr(np.ascontiguousarray(weights["embed"], np.uint16))))
         check(L.pia_model_set_norm(h, 0, NORM_FINAL, ptr(np.ascontiguousarray(weights["final_norm"], np.float32))))
@@ -416,8 +475,21 @@ class Model:
             check(L.pia_model_set_norm(h, i, NORM_FFN, ptr(np.ascontiguousarray(lw["ffn_norm"], np.float32))))
             for name in ("wq", "wk", "wv", "wo", "w1", "w2", "w3"):
                 self._set_proj(i, name, lw[name])
-        self.kv_ptr = None
-        self.layout = None
+
+    @classmethod
+    def from_safetensors(cls, ctx: Context, path, cfg: LlamaConfig | None = None, quantization: str = "int8",
+                         lm_head_int8: bool = False) -> "Model":
+        """ModelLoader::load_weights (src/model.rs:388-447) straight into device memory: a bf16
+        HF Llama checkpoint, projections widened ("f32") or quantized on the device ("int8");
+        the LM head stays f32 unless lm_head_int8. cfg defaults to the config.json beside
+        the checkpoint (LlamaConfig.beside_checkpoint)."""
+        if quantization not in ("f32", "int8"):
+            raise ValueError("quantization must be 'f32' or 'int8'")
+        cfg = cfg or LlamaConfig.beside_checkpoint(path)
+        m = cls(ctx, cfg, None)
+        check(lib().pia_model_load_safetensors(m.h, str(path).encode(), 1 if quantization == "int8" else 0,
+                                               1 if lm_head_int8 else 0))
+        return m
 
     def _set_proj(self, layer, name, p):
         if isinstance(p, tuple):
@@ -488,6 +560,31 @@ class Model:
         check(lib().pia_model_prefill(self.h, ptr(tok), tok.size, start_pos, ptr(t), len(table), ptr(logits),
                                       ptr(am)))
         return logits, int(am[0])
+
+    def verify_groups(self, groups, capacity: int = 0):
+        """Engine::run_groups + verification (src/engine.rs:702-783). `groups` is a list of
+        (pos, tokens, table): the held token at pos followed by its drafts, on the sequence's
+        block table. Returns (per-group predictions, per-group accepted count, per-group
+        corrected token, passes)."""
+        gs = (SpecGroup * max(1, len(groups)))()
+        toks, flat_tables = [], []
+        for g, (pos, tokens, table) in enumerate(groups):
+            gs[g] = SpecGroup(pos, len(tokens), len(toks), len(flat_tables), len(table))
+            toks += list(tokens)
+            flat_tables += list(table)
+        t = np.ascontiguousarray(np.asarray(toks or [0], np.uint32))
+        tb = np.ascontiguousarray(np.asarray(flat_tables or [0], np.int32))
+        pred = np.zeros(max(1, len(toks)), np.uint32)
+        acc = np.zeros(max(1, len(groups)), np.int64)
+        corr = np.zeros(max(1, len(groups)), np.uint32)
+        passes = I64()
+        check(lib().pia_model_verify_groups(self.h, C.cast(gs, P), len(groups), ptr(t), ptr(tb), capacity, ptr(pred),
+                                            ptr(acc), ptr(corr), C.byref(passes)))
+        out, off = [], 0
+        for _, tokens, _ in groups:
+            out.append([int(x) for x in pred[off:off + len(tokens)]])
+            off += len(tokens)
+        return out, [int(a) for a in acc[:len(groups)]], [int(c) for c in corr[:len(groups)]], passes.value
 
     def bench_class(self, cls: str, batch: int, reps: int = 5):
         """(us per launch, algorithmic bytes per launch) of one projection class at `batch`."""

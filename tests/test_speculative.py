@@ -1,0 +1,238 @@
+"""Speculative verification on the batched decode path (src/speculative.rs, the engine's
+plan_step / run_groups / commit, src/engine.rs:595-805) through the C ABI.
+
+CPU: PromptLookupDrafter and verify_greedy against the reference's own unit cases
+(src/speculative.rs:256-345) and against a brute-force search over every (length, start)
+match on random contexts. GPU: several positions of one sequence in one batch against the
+CPU oracle's decode_batch on the same entries (greedy tokens bit-exact, logits within 2e-3
+relative), and the reference's losslessness tests (tests/speculative_tests.rs): speculative
+output identical to greedy output token for token at draft depths 1, 2, 4, 8 on the golden
+fixture model, fewer passes on repetitive text, emitted == steps + accepted, and the token
+budget respected."""
+import numpy as np
+import pytest
+
+import pia
+from golden import fixture
+
+
+# ------------------------------------------------------------------------------------------
+# CPU: drafter and verification.
+# ------------------------------------------------------------------------------------------
+def test_verify_greedy_reference_cases():
+    assert pia.verify_greedy([10, 11, 12], [10, 11, 99, 13]) == ([10, 11], 99)
+    assert pia.verify_greedy([1, 2, 3], [1, 2, 3, 4]) == ([1, 2, 3], 4)
+    assert pia.verify_greedy([7, 7, 7], [1, 2, 3, 4]) == ([], 1)
+    assert pia.verify_greedy([], [42]) == ([], 42)
+    with pytest.raises(pia.PiaError, match="plus one more"):
+        pia.verify_greedy([1, 2], [1, 2])
+
+
+def test_prompt_lookup_reference_cases():
+    assert pia.prompt_lookup_draft([1, 2, 3, 4, 5, 9, 9, 1, 2], 3) == [3, 4, 5]
+    assert pia.prompt_lookup_draft([2, 3, 4, 7, 8, 2, 3], 2, 1, 8) == [4, 7]
+    assert pia.prompt_lookup_draft([1, 2, 3, 4, 5], 4) == []
+    assert pia.prompt_lookup_draft([], 4) == []
+    assert pia.prompt_lookup_draft([1], 4) == []
+    assert pia.prompt_lookup_draft([1, 2], 0) == []
+    ctx = list(range(40)) + list(range(4))
+    for k in range(8):
+        assert len(pia.prompt_lookup_draft(ctx, k)) <= k
+    with pytest.raises(pia.PiaError, match="at least one token"):
+        pia.prompt_lookup_draft([1, 2, 3], 2, 0, 4)
+
+
+def _brute_force_draft(ctx, k, lo, hi):
+    """Every earlier occurrence of every suffix length, ranked (longer first, then later
+    start first); the first one that leaves something to copy wins."""
+    n = len(ctx)
+    if k == 0 or n <= lo:
+        return []
+    cands = []
+    for m in range(lo, min(max(hi, lo), n - 1) + 1):
+        for start in range(0, n - m):
+            if ctx[start:start + m] == ctx[n - m:] and start + m < n - m:
+                cands.append((-m, -start))
+    if not cands:
+        return []
+    m, start = -min(cands)[0], -min(cands)[1]
+    return ctx[start + m:start + m + min(k, n - m - start - m)]
+
+
+def test_prompt_lookup_brute_force():
+    rng = np.random.default_rng(5)
+    for trial in range(400):
+        n = int(rng.integers(0, 40))
+        ctx = [int(x) for x in rng.integers(0, int(rng.integers(2, 6)), n)]
+        k = int(rng.integers(0, 9))
+        lo = int(rng.integers(1, 4))
+        hi = int(rng.integers(lo, 10))
+        assert pia.prompt_lookup_draft(ctx, k, lo, hi) == _brute_force_draft(ctx, k, lo, hi), (ctx, k, lo, hi)
+
+
+# ------------------------------------------------------------------------------------------
+# GPU.
+# ------------------------------------------------------------------------------------------
+@pytest.mark.gpu
+def test_multi_position_groups_match_oracle(ctx):
+    """Three sequences, each a held token plus drafts at consecutive positions on its own
+    (scattered) table, one sequence with no drafts; flattened into one batch, and also split
+    across passes of capacity 4 (a group straddling two passes)."""
+    from oracle import oracle as orc
+    cfg = pia.LlamaConfig(hidden=128, layers=2, heads=4, kv_heads=2, inter=344, vocab=512)
+    w = pia.synth_weights(cfg, seed=21)
+    bs, nb = 8, 40
+    rng = np.random.default_rng(21)
+    kv0 = (rng.standard_normal(orc.kv_floats(cfg, nb, bs), dtype=np.float32) * 0.5)
+    perm = rng.permutation(nb).tolist()
+    tables = [perm[0:6], perm[6:14], perm[14:20]]
+    groups = [(17, [5, 9, 9, 301], tables[0]), (40, [77], tables[1]), (3, [1, 2, 3, 4, 5, 6], tables[2])]
+    om_ = orc.OracleModel(cfg, w)
+    gm = pia.Model(ctx, cfg, w)
+    for capacity in (0, 4):
+        gm.kv_alloc(nb, bs)
+        gm.kv_upload(kv0)
+        kv = kv0.copy()
+        preds, acc, corr, passes = gm.verify_groups(groups, capacity)
+        toks = [t for _, ts, _ in groups for t in ts]
+        pos = [p + j for p, ts, _ in groups for j in range(len(ts))]
+        tabs = [tb for _, ts, tb in groups for _ in ts]
+        if capacity == 0:
+            lc = om_.decode(toks, pos, tabs, kv, nb, bs)
+        else:
+            lc = np.concatenate([om_.decode(toks[s:s + capacity], pos[s:s + capacity], tabs[s:s + capacity], kv, nb,
+                                            bs) for s in range(0, len(toks), capacity)])
+        ref = [orc.argmax(r) for r in lc]
+        flat = [t for p in preds for t in p]
+        print(f"capacity {capacity}: passes {passes} predictions {flat}", flush=True)
+        assert flat == ref
+        assert passes == (1 if capacity == 0 else (len(toks) + capacity - 1) // capacity)
+        off = 0
+        for g, (_, ts, _) in enumerate(groups):
+            a, c = pia.verify_greedy(ts[1:], ref[off:off + len(ts)])
+            assert acc[g] == len(a) and corr[g] == c
+            off += len(ts)
+        # The decode pass also returns logits through pia_model_decode; compare them once.
+        if capacity == 0:
+            gm.kv_upload(kv0)
+            lg, _ = gm.decode(toks, pos, tabs)
+            rel = float(np.max(np.abs(lg - lc)) / np.max(np.abs(lc)))
+            assert rel <= 2e-3, rel
+    gm.close()
+
+
+def _generate(model, prompts, max_tokens, draft_tokens, block_size=8, total_blocks=256, capacity=0):
+    """The reference engine's greedy loop (admit / plan_step / run_groups / commit,
+    src/engine.rs:485-805) with its memory manager, on the GPU model. Returns (tokens per
+    request, stats dict, steps)."""
+    model.kv_alloc(total_blocks, block_size)
+    kvm = pia.KvCacheManager(total_blocks, block_size, True)
+    eos = 2 ** 32 - 1
+    stats = dict(steps=0, drafted=0, accepted=0, emitted=0, passes=0)
+    waiting = list(enumerate(prompts))
+    active, done = [], {}
+    tick, next_id, engine_steps = 0, 0, 0
+    while waiting or active:
+        tick += 1
+        while waiting:  # admit
+            rid, toks = waiting[0]
+            adm = kvm.admit(next_id, toks, tick)
+            if adm is None:
+                break
+            waiting.pop(0)
+            table, (cached, _, _) = adm
+            resume = min(cached, len(toks) - 1)
+            _, am = model.prefill(toks[resume:], resume, table.blocks())
+            kvm.publish(table)
+            first = int(am)
+            seq = dict(id=next_id, rid=rid, ids=list(toks) + [first], gen=[first], table=table, fin=max_tokens <= 1)
+            next_id += 1
+            active.append(seq)
+        groups, owners = [], []  # plan_step
+        for seq in active:
+            if seq["fin"]:
+                continue
+            pos = len(seq["ids"]) - 1
+            room = max(0, max_tokens - len(seq["gen"]) - 1)
+            drafts = []
+            if draft_tokens > 0 and room > 0:
+                drafts = pia.prompt_lookup_draft(seq["ids"], min(draft_tokens, room))[:room]
+            span = len(drafts) + 1
+            while len(seq["table"]) < (pos + span + block_size - 1) // block_size:
+                assert kvm.append_block(seq["id"], seq["table"], tick)
+            for p in range(pos, pos + span):
+                kvm.ensure_writable(seq["id"], seq["table"], p, model.ctx, model.kv_ptr, model.layout)
+            kvm.touch(seq["id"], tick)
+            groups.append((pos, [seq["ids"][-1]] + drafts, seq["table"].blocks()))
+            owners.append(seq)
+        if groups:
+            preds, acc, corr, passes = model.verify_groups(groups, capacity)
+            stats["passes"] += passes
+            for g, seq in enumerate(owners):  # commit
+                drafts = groups[g][1][1:]
+                stats["steps"] += 1
+                stats["drafted"] += len(drafts)
+                stats["accepted"] += acc[g]
+                emitted = 0
+                for tok in drafts[:acc[g]] + [corr[g]]:
+                    if seq["fin"]:
+                        break
+                    seq["gen"].append(tok)
+                    seq["ids"].append(tok)
+                    emitted += 1
+                    if tok == eos or len(seq["gen"]) >= max_tokens:
+                        seq["fin"] = True
+                stats["emitted"] += emitted
+        for seq in [s for s in active if s["fin"]]:  # reclaim
+            done[seq["rid"]] = seq["gen"]
+            kvm.release(seq["id"])
+            active.remove(seq)
+        engine_steps += 1
+    return [done[i] for i in range(len(prompts))], stats, engine_steps
+
+
+def _fixture_model(ctx):
+    return pia.Model.from_safetensors(ctx, fixture.HERE / "tiny_llama.safetensors", quantization="f32")
+
+
+def _repetitive(tokens):
+    return list(tokens[:6]) * 6
+
+
+@pytest.mark.gpu
+def test_speculative_output_is_identical_to_greedy(ctx):
+    _, tokens, _, _ = fixture.load()
+    prompts = [tokens[:12], _repetitive(tokens), tokens[:20]]
+    m = _fixture_model(ctx)
+    m.kv_alloc(256, 8)
+    base, bstats, _ = _generate(m, prompts, 24, 0)
+    assert bstats["drafted"] == 0
+    for k in (1, 2, 4, 8):
+        spec, st, _ = _generate(m, prompts, 24, k)
+        print(f"k={k}: drafted {st['drafted']} accepted {st['accepted']} passes {st['passes']}", flush=True)
+        assert spec == base, f"draft depth {k} changed the generated text"
+    # Splitting the flattened groups across passes of 3 entries changes nothing either.
+    spec, _, _ = _generate(m, prompts, 24, 4, capacity=3)
+    assert spec == base
+    m.close()
+
+
+@pytest.mark.gpu
+def test_speculation_reduces_passes_and_keeps_accounting(ctx):
+    _, tokens, _, _ = fixture.load()
+    m = _fixture_model(ctx)
+    m.kv_alloc(256, 8)
+    _, base, _ = _generate(m, [_repetitive(tokens)], 32, 0)
+    _, spec, _ = _generate(m, [_repetitive(tokens)], 32, 4)
+    print(f"passes {base['passes']} -> {spec['passes']}; accepted {spec['accepted']}/{spec['drafted']}")
+    assert spec["accepted"] > 0 and spec["passes"] < base["passes"]
+    assert spec["emitted"] / spec["steps"] > 1.0
+    prompt = list(range(24))
+    b, _, _ = _generate(m, [prompt], 16, 0)
+    s, st, _ = _generate(m, [prompt], 16, 4)
+    assert b == s
+    assert st["emitted"] == st["steps"] + st["accepted"] and st["accepted"] <= st["drafted"]
+    for max_tokens in (1, 2, 3, 5, 7, 13):
+        out, _, _ = _generate(m, [_repetitive(tokens)], max_tokens, 4)
+        assert len(out[0]) == max_tokens
+    m.close()
