@@ -252,6 +252,43 @@ pia_status pia_model_set_decode_path(pia_model* m, int32_t path);
 int32_t pia_model_decode_path_used(const pia_model* m);
 
 /* ------------------------------------------------------------------------------------ */
+/* Sampling (src/sampling.rs).                                                            */
+/* ------------------------------------------------------------------------------------ */
+typedef struct pia_sampling { /* Sampler's settings (src/sampling.rs:43-52) */
+  float temperature; /* <= 0: greedy argmax, no draw */
+  float top_p;       /* >= 1: no nucleus cut */
+  int32_t top_k;     /* 0: disabled */
+  int32_t reserved;  /* must be 0 */
+} pia_sampling;
+
+/* Rng::new (src/sampling.rs:20-25): the xorshift64* state for a seed. */
+uint64_t pia_rng_new(uint64_t seed);
+
+/* Sampler::sample (src/sampling.rs:74-138) for n rows of logits (device, pitch ld floats):
+ * out[i] (device) = the token drawn for row i with params[i] (device), advancing the
+ * xorshift64* state rng_state[i] (device) by one draw when temperature > 0. Ranking is
+ * f32::total_cmp descending with equal logits in ascending index order (the reference's
+ * unstable sort leaves their order unspecified).
+ * mode 0 (PIA_SAMPLE_REFERENCE): the reference's arithmetic order -- a device sort, then the
+ *   f32 running sums in ranking order -- so the token is the reference's; uses a workspace of
+ *   about 28 bytes per logit held by the context, grown on demand (a grow synchronizes the
+ *   device).
+ * mode 1 (PIA_SAMPLE_EXACT_SUMS): no sort; radix searches with exact fixed-point sums. The
+ *   token differs from the reference's only where the draw lies within the reference's f32
+ *   summation rounding (up to vocab * 2^-24 relative) of a cumulative boundary. */
+enum { PIA_SAMPLE_REFERENCE = 0, PIA_SAMPLE_EXACT_SUMS = 1 };
+pia_status pia_sample_dev(pia_context* ctx, int32_t* out, const float* logits, int64_t ld, int64_t n, int64_t vocab,
+                          const pia_sampling* params, uint64_t* rng_state, int32_t mode, void* stream);
+
+/* Sample from the logits the last pia_model_decode (rows 0..n-1, n <= its batch) or
+ * pia_model_prefill (n = 1) left on the device, as pia_sample_dev does, with host arrays:
+ * params[n], rng_state[n] (advanced in place) and out[n]. The engine's per-sequence
+ * Sampler::sample on the batch logits (src/engine.rs:741-756), without copying logits to the
+ * host. */
+pia_status pia_model_sample(pia_model* m, const pia_sampling* params, uint64_t* rng_state, int64_t n, int32_t mode,
+                            int32_t* out);
+
+/* ------------------------------------------------------------------------------------ */
 /* Speculative verification (src/speculative.rs, src/engine.rs:595-761).                  */
 /* ------------------------------------------------------------------------------------ */
 /* PromptLookupDrafter::draft (src/speculative.rs:71-101): up to k tokens that followed the

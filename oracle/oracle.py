@@ -36,6 +36,12 @@ class Entry(C.Structure):
     _fields_ = [("pos", I64), ("start", I64), ("table_off", I64), ("table_len", I64)]
 
 
+_SIGS_SAMPLING = {
+    "orc_rng_new": (C.c_uint64, [C.c_uint64]),
+    "orc_rng_next_u64": (C.c_uint64, [C.POINTER(C.c_uint64)]),
+    "orc_rng_next_f32": (F32, [C.POINTER(C.c_uint64)]),
+    "orc_sample": (I64, [P, I64, F32, F32, I64, C.POINTER(C.c_uint64)]),
+}
 _SIGS = {
     "orc_set_threads": (None, [C.c_int]),
     "orc_threads": (C.c_int, []),
@@ -72,7 +78,7 @@ def lib():
         if not LIB_PATH.exists():
             build()
         L = C.CDLL(str(LIB_PATH))
-        for name, (res, args) in _SIGS.items():
+        for name, (res, args) in {**_SIGS, **_SIGS_SAMPLING}.items():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
@@ -252,3 +258,29 @@ class OracleModel:
 
 def kv_floats(cfg, num_blocks: int, block_size: int) -> int:
     return cfg.layers * num_blocks * block_size * cfg.kv_heads * 2 * cfg.head_dim
+
+
+class Rng:
+    """Rng (src/sampling.rs:15-41) over the oracle's restatement."""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64(lib().orc_rng_new(seed))
+
+    def next_u64(self) -> int:
+        return int(lib().orc_rng_next_u64(C.byref(self.state)))
+
+    def next_f32(self) -> float:
+        return float(lib().orc_rng_next_f32(C.byref(self.state)))
+
+
+class Sampler:
+    """Sampler (src/sampling.rs:43-138) over the oracle's restatement."""
+
+    def __init__(self, temperature: float, top_p: float, top_k: int, seed: int):
+        self.temperature, self.top_p, self.top_k = temperature, top_p, top_k
+        self.rng = Rng(seed)
+
+    def sample(self, logits) -> int:
+        x = np.ascontiguousarray(np.asarray(logits, np.float32))
+        return int(lib().orc_sample(_p(x), x.size, self.temperature, self.top_p, self.top_k, C.byref(self.rng.state)))
+

@@ -18,6 +18,7 @@
 //   decode_batch_into                 src/model.rs:1184-1207
 //   prefill_batched                   src/model.rs:1222-1255
 //   argmax                            src/sampling.rs:140-147
+//   Rng (xorshift64*), Sampler::sample src/sampling.rs:15-138
 // Rayon's row/lane parallelism is replaced by a fixed worker pool; it changes no arithmetic
 // (every output element is produced by exactly one task, as in the reference).
 //
@@ -629,6 +630,80 @@ void orc_prefill(const orc_model* m, const uint32_t* tokens, int64_t n, int64_t 
     last = len - 1;
   }
   matvec(m->lm_head, logits, &x[last * m->c.hidden]);
+}
+
+// ---------------------------------------------------------------------------------------
+// Sampling (src/sampling.rs).
+// ---------------------------------------------------------------------------------------
+// Rng::new (sampling.rs:20-25): the seed folded with a constant so that 0 is not a fixed point.
+uint64_t orc_rng_new(uint64_t seed) { return seed ^ 0x9E3779B97F4A7C15ull; }
+
+// Rng::next_u64 (sampling.rs:27-34): xorshift64* -- three xor-shifts of the state, output the
+// state times a 64-bit odd constant (wrapping).
+uint64_t orc_rng_next_u64(uint64_t* state) {
+  uint64_t x = *state;
+  x ^= x >> 12;
+  x ^= x << 25;
+  x ^= x >> 27;
+  *state = x;
+  return x * 0x2545F4914F6CDD1Dull;
+}
+
+// Rng::next_f32 (sampling.rs:36-40): the top 24 bits over 2^24, in [0, 1).
+float orc_rng_next_f32(uint64_t* state) {
+  return static_cast<float>(orc_rng_next_u64(state) >> 40) / static_cast<float>(1u << 24);
+}
+
+// Sampler::sample (sampling.rs:74-138). Rank by f32::total_cmp descending (the reference's
+// unstable sort leaves equal logits in an unspecified order; here they keep ascending index),
+// keep top_k, exponentiate relative to the top logit, normalize by the sequential f32 sum,
+// cut the nucleus at the first cumulative >= top_p and renormalize, then walk the cumulative
+// to the first value above one uniform draw. temperature <= 0: argmax, no draw.
+int64_t orc_sample(const float* logits, int64_t n, float temperature, float top_p, int64_t top_k,
+                   uint64_t* state) {
+  if (n <= 0) return -1;
+  if (temperature <= 0.0f) return orc_argmax(logits, n);
+  auto key = [](float f) {
+    int32_t b;
+    std::memcpy(&b, &f, 4);
+    return b ^ static_cast<int32_t>(static_cast<uint32_t>(b >> 31) >> 1);
+  };
+  std::vector<uint32_t> order(static_cast<size_t>(n));
+  for (int64_t i = 0; i < n; ++i) order[i] = static_cast<uint32_t>(i);
+  std::stable_sort(order.begin(), order.end(),
+                   [&](uint32_t a, uint32_t b) { return key(logits[a]) > key(logits[b]); });
+  const size_t keep = top_k == 0 ? order.size() : std::min<size_t>(static_cast<size_t>(top_k), order.size());
+  order.resize(keep);
+  const float inv_temp = 1.0f / temperature;
+  const float max_logit = logits[order[0]];
+  std::vector<float> probs(keep);
+  for (size_t i = 0; i < keep; ++i) probs[i] = expf((logits[order[i]] - max_logit) * inv_temp);
+  float total = 0.0f;
+  for (float p : probs) total += p;
+  for (float& p : probs) p /= total;
+  if (top_p < 1.0f) {
+    float cumulative = 0.0f;
+    size_t cut = probs.size();
+    for (size_t i = 0; i < probs.size(); ++i) {
+      cumulative += probs[i];
+      if (cumulative >= top_p) {
+        cut = i + 1;
+        break;
+      }
+    }
+    probs.resize(cut);
+    order.resize(cut);
+    float renorm = 0.0f;
+    for (float p : probs) renorm += p;
+    for (float& p : probs) p /= renorm;
+  }
+  const float target = orc_rng_next_f32(state);
+  float cumulative = 0.0f;
+  for (size_t i = 0; i < probs.size(); ++i) {
+    cumulative += probs[i];
+    if (target < cumulative) return order[i];
+  }
+  return order.back();
 }
 
 }  // extern "C"

@@ -8,12 +8,6 @@
 
 #include "paged_infer_amd.h"
 
-struct pia_context {
-  int device = 0;
-  int num_cus = 0;
-  hipStream_t stream = nullptr;
-};
-
 namespace pia {
 
 // Grow-only device allocation.
@@ -52,12 +46,24 @@ struct PinnedBuffer {
   void ensure(size_t need);
 };
 
+}  // namespace pia
+
+struct pia_context {
+  int device = 0;
+  int num_cus = 0;
+  hipStream_t stream = nullptr;
+  pia::DeviceBuffer sample_ws;  // sort keys / indices / probabilities of pia_sample_dev
+};
+
+namespace pia {
 hipStream_t stream_of(pia_context* ctx, void* stream);
 void check_layout(const pia_kv_layout* L);
 void quantize_rows_host(const float* w, int64_t rows, int64_t cols, int8_t* q, float* scales);
 // Fill projection slot `which` of `layer` from device bf16 rows [rows][cols]: kind 1 quantizes
 // them on the device (bit-exact with the host quantizer), kind 0 widens them to f32.
+// pia_sample_dev with the context's workspace, on stream st.
+void sample_with_context(pia_context* ctx, int32_t* out, const float* logits, int64_t ld, int64_t n, int64_t vocab,
+                         const pia_sampling* params, uint64_t* rng_state, int32_t mode, hipStream_t st);
 void model_set_proj_bf16_dev(pia_model* m, int64_t layer, int32_t which, int kind, const uint16_t* src, int64_t rows,
                              int64_t cols);
-
 }  // namespace pia

@@ -97,6 +97,8 @@ struct pia_model {
   int64_t cap = 0;  // rows of activation scratch
   DeviceBuffer x, xb, qkv, attn, h, logits, amax, attn_work, step, xq;
   int64_t mfma_min = kMfmaMinBatch;
+  int64_t logit_rows = 0;  // rows of `logits` the last decode / prefill wrote
+  DeviceBuffer samp;       // sampling parameters, generator states and drawn tokens
   PinnedBuffer pin, pin_out;
   Prof prof;
 
@@ -909,6 +911,7 @@ pia_status pia_model_decode(pia_model* m, const uint32_t* tokens, const int64_t*
     PIA_HIP(hipMemcpy2DAsync(logits, c.vocab * 4, m->logits.ptr, m->ld_v * 4, c.vocab * 4, batch,
                              hipMemcpyDeviceToHost, m->st()));
   m->last_path = step ? 1 : 0;
+  m->logit_rows = batch;
   m->read_argmax(argmax, batch, step);
   if (step && m->step_trace.ptr) m->print_step_trace();
   m->finish_prof();
@@ -953,9 +956,36 @@ pia_status pia_model_prefill(pia_model* m, const uint32_t* tokens, int64_t n, in
                    m->logits.as<float>(), m->ld_v, Epi::Store, m->amax.as<unsigned long long>());
   });
   if (logits) PIA_HIP(hipMemcpyAsync(logits, m->logits.ptr, c.vocab * 4, hipMemcpyDeviceToHost, m->st()));
+  m->logit_rows = 1;
   m->read_argmax(argmax, 1);
   m->finish_prof();
   PIA_API_END
 }
 
+pia_status pia_model_sample(pia_model* m, const pia_sampling* params, uint64_t* rng_state, int64_t n, int32_t mode,
+                            int32_t* out) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(m && params && rng_state && out, "null argument");
+  PIA_REQUIRE(n > 0 && n <= m->logit_rows, "sample: no logits for that many rows (decode or prefill first)");
+  for (int64_t i = 0; i < n; ++i) {
+    PIA_REQUIRE(params[i].top_k >= 0 && params[i].reserved == 0, "sample: bad sampling parameters");
+    PIA_REQUIRE(params[i].temperature == params[i].temperature && params[i].top_p == params[i].top_p,
+                "sample: NaN temperature or top_p");
+  }
+  PIA_HIP(hipSetDevice(m->ctx->device));
+  const size_t pb = static_cast<size_t>(n) * sizeof(pia_sampling), rb = static_cast<size_t>(n) * 8;
+  m->grow(m->samp, pb + rb + static_cast<size_t>(n) * 4);
+  char* d = static_cast<char*>(m->samp.ptr);
+  PIA_HIP(hipMemcpyAsync(d, params, pb, hipMemcpyHostToDevice, m->st()));
+  PIA_HIP(hipMemcpyAsync(d + pb, rng_state, rb, hipMemcpyHostToDevice, m->st()));
+  sample_with_context(m->ctx, reinterpret_cast<int32_t*>(d + pb + rb), m->logits.as<float>(), m->ld_v, n,
+                      m->cfg.vocab, reinterpret_cast<const pia_sampling*>(d), reinterpret_cast<uint64_t*>(d + pb), mode,
+                      m->st());
+  PIA_HIP(hipMemcpyAsync(rng_state, d + pb, rb, hipMemcpyDeviceToHost, m->st()));
+  PIA_HIP(hipMemcpyAsync(out, d + pb + rb, static_cast<size_t>(n) * 4, hipMemcpyDeviceToHost, m->st()));
+  PIA_HIP(hipStreamSynchronize(m->st()));
+  PIA_API_END
+}
+
 }  // extern "C"
+

@@ -95,6 +95,26 @@ void quantize_rows_host(const float* w, int64_t rows, int64_t cols, int8_t* q, f
 
 using namespace pia;
 
+namespace pia {
+void sample_with_context(pia_context* ctx, int32_t* out, const float* logits, int64_t ld, int64_t n, int64_t vocab,
+                         const pia_sampling* params, uint64_t* rng_state, int32_t mode, hipStream_t st) {
+  PIA_REQUIRE(n >= 0, "negative row count");
+  if (n == 0) return;
+  PIA_REQUIRE(out && logits && params && rng_state, "null argument");
+  PIA_REQUIRE(mode == PIA_SAMPLE_REFERENCE || mode == PIA_SAMPLE_EXACT_SUMS, "unknown sampling mode");
+  size_t ws = 0;
+  if (mode == PIA_SAMPLE_REFERENCE) {
+    PIA_REQUIRE(vocab > 0 && n * vocab < (int64_t(1) << 31), "sample: rows x vocabulary too large for one sort");
+    ws = sample_workspace_bytes(n, vocab);
+    if (ctx->sample_ws.bytes < ws) {
+      PIA_HIP(hipDeviceSynchronize());  // the old workspace may still be in use by queued work
+      ctx->sample_ws.ensure(ws);
+    }
+  }
+  launch_sample(logits, ld, n, vocab, params, rng_state, out, mode, ctx->sample_ws.ptr, ctx->sample_ws.bytes, st);
+}
+}  // namespace pia
+
 extern "C" {
 
 const char* pia_last_error(void) { return g_last_error.c_str(); }
@@ -183,6 +203,17 @@ pia_status pia_quantize_rows_i8_dev(pia_context* ctx, const float* w, int64_t ro
   PIA_REQUIRE(ctx, "null context");
   PIA_REQUIRE(rows >= 0 && cols >= 0, "negative shape");
   launch_quantize_rows(w, rows, cols, q, scales, stream_of(ctx, stream));
+  PIA_API_END
+}
+
+uint64_t pia_rng_new(uint64_t seed) { return seed ^ 0x9E3779B97F4A7C15ull; }
+
+pia_status pia_sample_dev(pia_context* ctx, int32_t* out, const float* logits, int64_t ld, int64_t n, int64_t vocab,
+                          const pia_sampling* params, uint64_t* rng_state, int32_t mode, void* stream) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx, "null context");
+  PIA_HIP(hipSetDevice(ctx->device));
+  sample_with_context(ctx, out, logits, ld, n, vocab, params, rng_state, mode, stream_of(ctx, stream));
   PIA_API_END
 }
 

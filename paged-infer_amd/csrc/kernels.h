@@ -114,6 +114,13 @@ void launch_swiglu(const float* gu, int64_t ldgu, float* h, int64_t ldh, int64_t
 void launch_argmax(const float* logits, int64_t ld, int32_t* out, int64_t n, int64_t vocab, hipStream_t st);
 
 void launch_quantize_rows(const float* w, int64_t rows, int64_t cols, int8_t* q, float* scales, hipStream_t st);
+// Sampler::sample on the device (sampling.hip). mode 0: the reference's arithmetic order (a
+// device sort, then in-order f32 sums; needs sample_workspace_bytes(n, vocab) of workspace);
+// mode 1: radix search with exact fixed-point sums (no workspace).
+size_t sample_workspace_bytes(int64_t n, int64_t vocab);
+void launch_sample(const float* logits, int64_t ld, int64_t n, int64_t vocab, const pia_sampling* params,
+                   uint64_t* rng, int32_t* out, int mode, void* workspace, size_t workspace_bytes, hipStream_t st);
+
 // Checkpoint loading: bf16 rows [rows][cols] quantized (bit-exact with launch_quantize_rows of
 // the widened rows) or widened, source row r written to destination row r * row_step.
 void launch_quantize_rows_bf16(const uint16_t* w, int64_t rows, int64_t cols, int8_t* q, int64_t ldq, float* scales,

@@ -53,6 +53,26 @@ class KvmStats(C.Structure):
                 ("total_blocks", C.c_int64), ("active_sequences", C.c_int64), ("cached_entries", C.c_int64)]
 
 
+class Sampling(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int32), ("reserved", C.c_int32)]
+
+
+SAMPLING_DTYPE = np.dtype([("temperature", "<f4"), ("top_p", "<f4"), ("top_k", "<i4"), ("reserved", "<i4")])
+
+
+def sampling_array(params) -> np.ndarray:
+    """[(temperature, top_p, top_k), ...] as a pia_sampling array."""
+    a = np.zeros(len(params), SAMPLING_DTYPE)
+    for i, (t, p, k) in enumerate(params):
+        a[i] = (t, p, k, 0)
+    return a
+
+
+def rng_new(seed: int) -> int:
+    """Rng::new (src/sampling.rs:20-25): the xorshift64* state for a seed."""
+    return int(lib().pia_rng_new(seed))
+
+
 class SpecGroup(C.Structure):
     _fields_ = [("pos", C.c_int64), ("n_tokens", C.c_int64), ("tokens_off", C.c_int64), ("table_off", C.c_int64),
                 ("table_len", C.c_int64)]
@@ -115,6 +135,9 @@ _SIGS = {
     "pia_model_set_proj_f32": (I32, [P, I64, I32, P]),
     "pia_model_weight_bytes": (I64, [P]),
     "pia_model_get_config": (I32, [P, C.POINTER(ModelConfig)]),
+    "pia_rng_new": (U64, [U64]),
+    "pia_sample_dev": (I32, [P, P, P, I64, I64, I64, P, P, I32, P]),
+    "pia_model_sample": (I32, [P, P, P, I64, I32, P]),
     "pia_prompt_lookup_draft": (I32, [P, I64, I64, I64, I64, P, C.POINTER(I64)]),
     "pia_verify_greedy": (I32, [P, I64, P, I64, C.POINTER(I64), C.POINTER(C.c_uint32)]),
     "pia_model_verify_groups": (I32, [P, P, I64, P, P, I64, P, P, P, C.POINTER(I64)]),
@@ -287,6 +310,29 @@ class DeviceArray:
             self.free()
         except Exception:
             pass
+
+
+SAMPLE_REFERENCE, SAMPLE_EXACT_SUMS = 0, 1
+
+
+def sample_rows(ctx: Context, logits: np.ndarray, params, rng_state: np.ndarray, draws: int = 1,
+                mode: int = SAMPLE_REFERENCE):
+    """pia_sample_dev over host logits [n][vocab]: `draws` consecutive samples per row (the
+    generator state advancing on the device between them). Returns (tokens [draws][n], final
+    rng states)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    n, vocab = logits.shape
+    dl, dp = ctx.to_device(logits), ctx.to_device(sampling_array(params))
+    dr = ctx.to_device(np.ascontiguousarray(rng_state, np.uint64))
+    do = ctx.empty((n,), np.int32)
+    outs = []
+    for _ in range(draws):
+        check(lib().pia_sample_dev(ctx.h, do.ptr, dl.ptr, vocab, n, vocab, dp.ptr, dr.ptr, mode, None))
+        outs.append(do.numpy())
+    states = dr.numpy()
+    for d in (dl, dp, dr, do):
+        d.free()
+    return np.stack(outs), states
 
 
 BENCH_NORM, BENCH_SWIGLU, BENCH_ADD, BENCH_MFMA = 1, 2, 4, 8
@@ -560,6 +606,15 @@ class Model:
         check(lib().pia_model_prefill(self.h, ptr(tok), tok.size, start_pos, ptr(t), len(table), ptr(logits),
                                       ptr(am)))
         return logits, int(am[0])
+
+    def sample(self, params, rng_state: np.ndarray, mode: int = 0) -> list[int]:
+        """Sampler::sample (src/sampling.rs:74-138) on the device for the first len(params) rows
+        of the last decode's (or prefill's) logits; rng_state (uint64 [n]) advances in place."""
+        a = sampling_array(params)
+        assert rng_state.dtype == np.uint64 and rng_state.flags["C_CONTIGUOUS"] and rng_state.size == len(params)
+        out = np.empty(len(params), np.int32)
+        check(lib().pia_model_sample(self.h, ptr(a), ptr(rng_state), len(params), mode, ptr(out)))
+        return [int(t) for t in out]
 
     def verify_groups(self, groups, capacity: int = 0):
         """Engine::run_groups + verification (src/engine.rs:702-783). `groups` is a list of
