@@ -10,7 +10,10 @@ blocks assigned by a random permutation of the pool), the dominant kernel's roof
 HIP events on the library's stream, and the CPU baseline (the oracle's restatement of the
 reference's rayon + AVX2 path) timed on a bounded sample on this host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-b32] [--no-cpu]
+Also (same line): device sampling latency per mode, the cost of a speculative verification
+pass against a plain step, and checkpoint loading throughput.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-b32] [--no-cpu] [--no-extras]
 """
 from __future__ import annotations
 
@@ -159,6 +162,112 @@ def run_b32(ctx, cfg, weights, steps, warmup, batch=32):
                 attn_gbs=(attn_bytes / 1e9) / (attn_ms / 1e3) if attn_ms else None,
                 gemv_ms=gemv_ms, attn_ms=attn_ms,
                 gate_up_gbs=gu["bytes_per_launch"] / (gu["us_per_launch"] * 1e3))
+
+
+def _timed(ctx, fn, reps):
+    fn()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    ctx.sync()
+    return (time.perf_counter() - t0) / reps
+
+
+def run_sampling(ctx, vocab, reps=20):
+    """Device sampling (Sampler::sample) over TinyLlama-vocabulary logits: microseconds per
+    call (host clock around `reps` back-to-back calls on the library stream), per mode, batch
+    and setting."""
+    rng = np.random.default_rng(SEED + 7)
+    res = {}
+    for batch in (1, 32):
+        logits = (rng.standard_normal((batch, vocab)) * 2.0).astype(np.float32)
+        dl, do = ctx.to_device(logits), ctx.empty((batch,), np.int32)
+        dr = ctx.to_device(np.array([pia.rng_new(i) for i in range(batch)], np.uint64))
+        for name, prm in (("t0.8_p0.9_k40", (0.8, 0.9, 40)), ("t1.0_full_vocab", (1.0, 1.0, 0))):
+            dp = ctx.to_device(pia.sampling_array([prm] * batch))
+            for mode, mname in ((pia.SAMPLE_REFERENCE, "reference_order"), (pia.SAMPLE_EXACT_SUMS, "exact_sums")):
+                call = lambda: pia.check(pia.lib().pia_sample_dev(ctx.h, do.ptr, dl.ptr, vocab, batch, vocab, dp.ptr,
+                                                                   dr.ptr, mode, None))
+                res[f"b{batch}_{name}_{mname}_us"] = round(1e6 * _timed(ctx, call, reps), 1)
+            dp.free()
+        for d in (dl, do, dr):
+            d.free()
+    return res
+
+
+def run_spec_verify(ctx, cfg, weights, prompt_len=512, reps=20):
+    """Cost of one speculative verification pass (pia_model_verify_groups) of the held token
+    plus K drafts of one sequence at context 512, against a plain batch-1 step (K = 0)."""
+    bs = 16
+    nb = (prompt_len + 64 + bs - 1) // bs
+    table = list(range(nb))
+    model = pia.Model(ctx, cfg, weights)
+    model.kv_alloc(nb, bs)
+    prompt = np.random.default_rng(SEED + 11).integers(0, cfg.vocab, prompt_len).tolist()
+    _, tok = model.prefill(prompt, 0, table, want_logits=False)
+    res = {}
+    for k in (0, 1, 4, 8):
+        group = [(prompt_len, [tok] + prompt[:k], table)]
+        res[f"k{k}_ms_per_pass"] = round(1e3 * _timed(ctx, lambda: model.verify_groups(group), reps), 4)
+    res["k4_cost_vs_k0"] = round(res["k4_ms_per_pass"] / res["k0_ms_per_pass"], 3)
+    model.close()
+    return res
+
+
+def run_loader(ctx, cfg, layers=4):
+    """pia_model_load_safetensors on a TinyLlama-shaped bf16 checkpoint cut to `layers` layers
+    (same per-layer shapes, full embedding and LM head), written to /dev/shm: seconds and
+    checkpoint GB/s, int8 (device quantizer) and f32."""
+    import struct
+    hd = cfg.hidden // cfg.heads
+    kvd = cfg.kv_heads * hd
+    rng = np.random.default_rng(SEED + 13)
+
+    def bf(shape):
+        n = int(np.prod(shape))
+        return pia.f32_to_bf16((rng.standard_normal(n, dtype=np.float32) * 0.02).reshape(shape))
+
+    shapes = {"model.embed_tokens.weight": (cfg.vocab, cfg.hidden), "model.norm.weight": (cfg.hidden,),
+              "lm_head.weight": (cfg.vocab, cfg.hidden)}
+    for i in range(layers):
+        p = f"model.layers.{i}"
+        shapes.update({f"{p}.input_layernorm.weight": (cfg.hidden,),
+                       f"{p}.post_attention_layernorm.weight": (cfg.hidden,),
+                       f"{p}.self_attn.q_proj.weight": (cfg.hidden, cfg.hidden),
+                       f"{p}.self_attn.k_proj.weight": (kvd, cfg.hidden),
+                       f"{p}.self_attn.v_proj.weight": (kvd, cfg.hidden),
+                       f"{p}.self_attn.o_proj.weight": (cfg.hidden, cfg.hidden),
+                       f"{p}.mlp.gate_proj.weight": (cfg.inter, cfg.hidden),
+                       f"{p}.mlp.down_proj.weight": (cfg.hidden, cfg.inter),
+                       f"{p}.mlp.up_proj.weight": (cfg.inter, cfg.hidden)})
+    header, off = {}, 0
+    for name, shp in shapes.items():
+        n = 2 * int(np.prod(shp))
+        header[name] = {"dtype": "BF16", "shape": list(shp), "data_offsets": [off, off + n]}
+        off += n
+    hj = json.dumps(header).encode()
+    hj += b" " * (-len(hj) % 8)
+    path = Path("/dev/shm") / f"pia_bench_{os.getpid()}.safetensors"
+    try:
+        with open(path, "wb") as f:
+            f.write(struct.pack("<Q", len(hj)))
+            f.write(hj)
+            for shp in shapes.values():
+                f.write(bf(shp).tobytes())
+        lcfg = pia.LlamaConfig(cfg.hidden, layers, cfg.heads, cfg.kv_heads, cfg.inter, cfg.vocab)
+        res = {"checkpoint_bytes": off, "layers": layers}
+        for quant in ("int8", "f32"):
+            t0 = time.perf_counter()
+            m = pia.Model.from_safetensors(ctx, path, lcfg, quantization=quant, lm_head_int8=quant == "int8")
+            ctx.sync()
+            dt = time.perf_counter() - t0
+            m.close()
+            res[f"{quant}_s"] = round(dt, 3)
+            res[f"{quant}_GB_per_s"] = round(off / dt / 1e9, 2)
+        return res
+    finally:
+        path.unlink(missing_ok=True)
 
 
 def run_c4_prefill(ctx, cfg, weights, seqs=8, seq_len=2048):
@@ -385,6 +494,8 @@ def main():
     ap.add_argument("--no-c5", action="store_true", help="skip configs[4] (Llama-3-8B batch 64, prefix + COW)")
     ap.add_argument("--c5-steps", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the sampling / speculative-verification / checkpoint-loading measurements")
     ap.add_argument("--sweep", action="store_true", help="also time each projection shape alone")
     ap.add_argument("--only-b32", action="store_true", help="run only the batch-32 decode (profiling aid)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -462,6 +573,11 @@ def main():
                                                              st32["nb"], st32["kv"], st32["gpu_argmax"], 10.0,
                                                              "TinyLlama shape, configs[2] contexts and tables")
         st32 = None
+    if not args.no_extras:
+        log("device sampling, speculative verification, checkpoint loading")
+        out["sampling_us"] = run_sampling(ctx, cfg.vocab)
+        out["spec_verify"] = run_spec_verify(ctx, cfg, weights)
+        out["loader"] = run_loader(ctx, cfg)
     if not args.no_c4:
         log("8 x 2048-token prefill (configs[3])")
         c4 = run_c4_prefill(ctx, cfg, weights)

@@ -26,7 +26,7 @@ inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 // Rows up to which RMSNorm is fused into the projection that consumes it.
 constexpr int64_t kFusedNormRows = 64;
 // Batch from which int8 projections run on the matrix cores instead of the streaming GEMV.
-constexpr int64_t kMfmaMinBatch = 8;
+constexpr int64_t kMfmaMinBatch = 5;
 
 struct Proj {
   int kind = -1;  // -1 unset, 0 f32, 1 int8
@@ -592,6 +592,8 @@ pia_status pia_model_create(pia_context* ctx, const pia_model_config* cfg, pia_m
   m->ld_i = round_up(c.inter, 16);
   m->ld_v = round_up(c.vocab, 16);
   m->layers.resize(c.layers);
+  // Diagnostic override of the batch from which decode projections use the matrix cores.
+  if (const char* e = std::getenv("PIA_MFMA_MIN_BATCH")) m->mfma_min = std::max<int64_t>(2, std::atoll(e));
   *out = m;
   PIA_API_END
 }

@@ -128,6 +128,88 @@ __global__ __launch_bounds__(kThreads) void k_xdigits(const float* __restrict__ 
   if (threadIdx.x == 0) pow2[b] = ldexpf(1.0f, -sh);
 }
 
+// The same digits with one wavefront per activation row (four rows per workgroup): shuffle
+// reductions only, 16-byte loads, four digits per 32-bit store. For rows of up to
+// 64 * 4 * kV4 <= 8192 floats with cols % 4 == 0 and 16-byte aligned rows; the row is held
+// in registers between the reductions and the digit split. Longer rows keep one workgroup
+// per row (k_xdigits), which spreads them over more lanes.
+template <int kV4>
+__global__ __launch_bounds__(256) void k_xdigits_wave(const float* __restrict__ x, int64_t ldx,
+                                                      const float* __restrict__ nw, float eps, int cols, int batch,
+                                                      int groups, int kpad, int8_t* __restrict__ dig,
+                                                      float* __restrict__ pow2) {
+  const int lane = threadIdx.x & 63;
+  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b >= groups) return;
+  int* d0 = reinterpret_cast<int*>(dig + static_cast<int64_t>(3 * b) * kpad);
+  int* d1 = d0 + kpad / 4;
+  int* d2 = d1 + kpad / 4;
+  const int n4 = cols >> 2, kp4 = kpad >> 2;
+  if (b >= batch) {
+    for (int i = lane; i < kp4; i += 64) d0[i] = d1[i] = d2[i] = 0;
+    if (lane == 0) pow2[b] = 0.0f;
+    return;
+  }
+  const float4* x4 = reinterpret_cast<const float4*>(x + static_cast<int64_t>(b) * ldx);
+  float4 v[kV4];
+#pragma unroll
+  for (int u = 0; u < kV4; ++u) {
+    const int i = lane + 64 * u;
+    v[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (nw) {
+    const float4* w4 = reinterpret_cast<const float4*>(nw);
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kV4; ++u) ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+#pragma unroll
+    for (int u = 0; u < kV4; ++u) {
+      const int i = lane + 64 * u;
+      if (i < n4) {
+        const float4 w = w4[i];
+        v[u] = make_float4((v[u].x * inv) * w.x, (v[u].y * inv) * w.y, (v[u].z * inv) * w.z, (v[u].w * inv) * w.w);
+      }
+    }
+  }
+  float m = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kV4; ++u) m = fmaxf(m, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  int e = 0;
+  if (m > 0.0f) (void)frexpf(m, &e);  // m = f * 2^e, f in [0.5, 1): max|x| < 2^e
+  const int sh = 22 - e;
+  auto split = [&](float f, int& a0, int& a1, int& a2) {
+    const int q = static_cast<int>(rintf(ldexpf(f, sh)));  // |q| <= 2^22
+    a0 = ((q + 128) & 255) - 128;
+    const int q1 = (q - a0) >> 8;
+    a1 = ((q1 + 128) & 255) - 128;
+    a2 = (q1 - a1) >> 8;  // |a2| <= 64
+  };
+  auto pack = [](int a, int b_, int c, int d) {
+    return (a & 255) | ((b_ & 255) << 8) | ((c & 255) << 16) | (d << 24);
+  };
+#pragma unroll
+  for (int u = 0; u < kV4; ++u) {
+    const int i = lane + 64 * u;
+    if (i < n4) {
+      int a[4], bb[4], c[4];
+      split(v[u].x, a[0], bb[0], c[0]);
+      split(v[u].y, a[1], bb[1], c[1]);
+      split(v[u].z, a[2], bb[2], c[2]);
+      split(v[u].w, a[3], bb[3], c[3]);
+      d0[i] = pack(a[0], a[1], a[2], a[3]);
+      d1[i] = pack(bb[0], bb[1], bb[2], bb[3]);
+      d2[i] = pack(c[0], c[1], c[2], c[3]);
+    }
+  }
+  for (int i = n4 + lane; i < kp4; i += 64) d0[i] = d1[i] = d2[i] = 0;  // the k-step padding
+  if (lane == 0) pow2[b] = ldexpf(1.0f, -sh);
+}
+
 enum { kEpiStore = 0, kEpiAdd = 1, kEpiSwiglu = 2 };
 
 __device__ inline uint32_t order_key(float f) {
@@ -590,8 +672,23 @@ void launch_xdigits(const float* x, int64_t ldx, const float* norm_w, float eps,
   int8_t* dig = static_cast<int8_t*>(xq);
   float* pow2 = reinterpret_cast<float*>(dig + (n * kpad + 255) / 256 * 256);
   const int64_t groups = n / 3;  // digit-column triples (batch rows, padded with zeros)
-  hipLaunchKernelGGL(k_xdigits, dim3(static_cast<unsigned>(groups)), dim3(kThreads), 0, st, x, ldx, norm_w, eps,
-                     static_cast<int>(cols), static_cast<int>(batch), static_cast<int>(kpad), dig, pow2);
+  const bool vec = cols % 4 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                   (!norm_w || (reinterpret_cast<uintptr_t>(norm_w) & 15) == 0);
+  const int64_t v4 = (cols / 4 + 63) / 64;  // float4 per lane
+  if (vec && v4 <= 32) {
+    const dim3 grid(static_cast<unsigned>((groups + 3) / 4));
+#define PIA_XDW(V)                                                                                            \
+  hipLaunchKernelGGL(k_xdigits_wave<V>, grid, dim3(256), 0, st, x, ldx, norm_w, eps, static_cast<int>(cols), \
+                     static_cast<int>(batch), static_cast<int>(groups), static_cast<int>(kpad), dig, pow2)
+    if (v4 <= 8) PIA_XDW(8);
+    else if (v4 <= 16) PIA_XDW(16);
+    else if (v4 <= 24) PIA_XDW(24);
+    else PIA_XDW(32);
+#undef PIA_XDW
+  } else {
+    hipLaunchKernelGGL(k_xdigits, dim3(static_cast<unsigned>(groups)), dim3(kThreads), 0, st, x, ldx, norm_w, eps,
+                       static_cast<int>(cols), static_cast<int>(batch), static_cast<int>(kpad), dig, pow2);
+  }
   PIA_HIP(hipGetLastError());
 }
 

@@ -11,6 +11,8 @@
 //   - epilogue residual add (src/model.rs:1127-1129, 1165-1167): out += proj;
 //   - epilogue SwiGLU (src/math.rs:293-302): gate and up rows are interleaved in HBM
 //     (row 2i = gate i, row 2i+1 = up i) and the wave that owns both writes silu(g) * u.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -88,6 +90,7 @@ __device__ inline float wave_sum(float v) {
 constexpr int kWaves = 4;  // wavefronts per workgroup
 constexpr int64_t kMaxStagedCols = 16384;  // batch-1 vectors up to this length are staged in LDS
 constexpr int kMaxNormBatch = 64;
+constexpr int64_t kMaxGemvnBatch = 4;  // batches up to this size take the LDS-staged kernel
 
 enum { kEpiStore = 0, kEpiAdd = 1, kEpiSwiglu = 2 };
 
@@ -478,6 +481,241 @@ void go1_unr(const GemvArgs& g, hipStream_t st) {
   else go1_epi<R, 8>(g, st);
 }
 
+// Small-batch (2..NB rows) int8 projection: the batch-1 kernel's scheme with every batch row
+// staged in LDS (normalized there when RMSNorm is fused), so each weight byte is fetched once
+// and applied to all NB rows from registers. Row b of the batch lives at xs + b * stride.
+constexpr int64_t kMaxGemvnSmem = 156 * 1024;  // LDS a workgroup of this kernel may take
+
+__host__ __device__ inline int64_t gemvn_stride(int64_t cols) {
+  const int64_t kpad = (cols + 1023) / 1024 * 1024;
+  return kpad + kpad / 16;
+}
+
+template <int R, int NB, int UNR, int EPI, bool NORM, bool AMAX>
+__global__ __launch_bounds__(64 * kWaves) void k_gemvn(const int8_t* __restrict__ W, int64_t ldw,
+                                                       const float* __restrict__ S, const float* __restrict__ X,
+                                                       int64_t ldx, const float* __restrict__ NW, float eps,
+                                                       float* __restrict__ O, int64_t osb, int64_t osr, int rows,
+                                                       int cols, int batch, unsigned long long* __restrict__ amax) {
+  extern __shared__ float xs[];
+  __shared__ float red[NB][kWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * kWaves + wave) * R;
+  constexpr int kStep = 64 * 16 * UNR;
+  const int n4 = cols >> 2;
+  const int kpad = (cols + 1023) / 1024 * 1024;
+  const int stride = static_cast<int>(gemvn_stride(cols));
+
+  // 1. The first batch of weights, in flight while the activations are staged.
+  const int8_t* wrow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) wrow[r] = W + static_cast<int64_t>(min(row0 + r, rows - 1)) * ldw;
+  Raw<int8_t, 16> raw[UNR][R];
+  auto load_batch = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int c = base + (u * 64 + lane) * 16;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (c < cols) raw[u][r].load(wrow[r] + c);
+        else raw[u][r].zero();
+      }
+    }
+  };
+  load_batch(0);
+
+  // 2. Activation rows into LDS (zeros for rows past `batch` and for the column padding), with
+  // each row's sum of squares.
+  float ss[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    ss[b] = 0.0f;
+    float* xb = xs + b * stride;
+    const float4* X4 = reinterpret_cast<const float4*>(X + static_cast<int64_t>(b) * ldx);
+    for (int i = threadIdx.x; i < n4; i += 64 * kWaves) {
+      const float4 v = b < batch ? X4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      float* d = xb + xs_index(4 * i);
+      d[0] = v.x, d[1] = v.y, d[2] = v.z, d[3] = v.w;
+      ss[b] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    for (int c = cols + threadIdx.x; c < kpad; c += 64 * kWaves) xb[xs_index(c)] = 0.0f;
+  }
+  if constexpr (NORM) {
+    // RMSNorm (src/math.rs:4-22) of every row: x * (1/rms) * w, in that order.
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float t = wave_sum(ss[b]);
+      if (lane == 0) red[b][wave] = t;
+    }
+    __syncthreads();
+    const float4* NW4 = reinterpret_cast<const float4*>(NW);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float t = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) t += red[b][w];
+      const float inv = 1.0f / sqrtf(t / static_cast<float>(cols) + eps);
+      float* xb = xs + b * stride;
+      for (int i = threadIdx.x; i < n4; i += 64 * kWaves) {
+        float* d = xb + xs_index(4 * i);
+        const float4 w = NW4[i];
+        d[0] = (d[0] * inv) * w.x, d[1] = (d[1] * inv) * w.y, d[2] = (d[2] * inv) * w.z, d[3] = (d[3] * inv) * w.w;
+      }
+    }
+  }
+  __syncthreads();
+  const bool active = row0 < rows;
+
+  // 3. Stream the rows against the staged batch.
+  float acc[R][NB];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[r][b] = 0.0f;
+  for (int base = 0; active && base < cols; base += kStep) {
+    if (base != 0) load_batch(base);
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int c = base + (u * 64 + lane) * 16;
+      if (c < cols) {
+        float w[R][16];
+#pragma unroll
+        for (int r = 0; r < R; ++r) raw[u][r].widen(w[r]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const float4* xp = reinterpret_cast<const float4*>(xs + b * stride + xs_index(c));
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float4 v = xp[q];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              acc[r][b] = __builtin_fmaf(w[r][4 * q], v.x, acc[r][b]);
+              acc[r][b] = __builtin_fmaf(w[r][4 * q + 1], v.y, acc[r][b]);
+              acc[r][b] = __builtin_fmaf(w[r][4 * q + 2], v.z, acc[r][b]);
+              acc[r][b] = __builtin_fmaf(w[r][4 * q + 3], v.w, acc[r][b]);
+            }
+          }
+        }
+      }
+    }
+  }
+
+  // 4. Lane r * NB + b holds row0 + r for batch row b.
+  float mine = 0.0f;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float t = wave_sum(acc[r][b]);
+      if (lane == r * NB + b) mine = t;
+    }
+  const int r_l = lane / NB, b_l = lane % NB;
+  const int row = row0 + r_l;
+  if constexpr (EPI == kEpiSwiglu) {
+    const float up = __shfl_down(mine, NB, 64);
+    if (active && lane < R * NB && (r_l & 1) == 0 && row + 1 < rows && b_l < batch) {
+      const float g = mine * S[row];
+      const float u = up * S[row + 1];
+      const float silu = g / (1.0f + expf(-g));
+      O[static_cast<int64_t>(b_l) * osb + static_cast<int64_t>(row >> 1) * osr] = silu * u;
+    }
+  } else {
+    const bool valid = active && lane < R * NB && row < rows && b_l < batch;
+    float v = 0.0f;
+    if (valid) {
+      v = mine * S[row];
+      float* o = O + static_cast<int64_t>(b_l) * osb + static_cast<int64_t>(row) * osr;
+      if (EPI == kEpiAdd) *o = *o + v;
+      else *o = v;
+    }
+    if constexpr (AMAX) {
+      // Per batch row: max of (order key, row) over the workgroup, one atomic per row.
+      __shared__ unsigned long long wbest[NB][kWaves];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        unsigned long long cand = 0;
+        if (valid && b_l == b)
+          cand = (static_cast<unsigned long long>(order_key(v)) << 32) | static_cast<uint32_t>(row);
+        cand = wave_max_u64(cand);
+        if (lane == 0) wbest[b][wave] = cand;
+      }
+      __syncthreads();
+      if (threadIdx.x < NB && static_cast<int>(threadIdx.x) < batch) {
+        unsigned long long m = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) m = wbest[threadIdx.x][w] > m ? wbest[threadIdx.x][w] : m;
+        if (m) atomicMax(&amax[threadIdx.x * kArgmaxSlots + (blockIdx.x & (kArgmaxSlots - 1))], m);
+      }
+    }
+  }
+}
+
+template <int R, int NB, int UNR, int EPI>
+void gon(const GemvArgs& g, int64_t b0, int64_t nb, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((g.rows + kWaves * R - 1) / (kWaves * R)));
+  const size_t smem = static_cast<size_t>(NB * gemvn_stride(g.cols)) * 4;
+  const auto* w = static_cast<const int8_t*>(g.W);
+  const float* x = g.x + b0 * g.ldx;
+  float* o = g.out + b0 * g.osb;
+  unsigned long long* am = g.amax ? g.amax + b0 * kArgmaxSlots : nullptr;
+#define PIA_GEMVN(NORM, AMAX)                                                                                \
+  do {                                                                                                       \
+    static bool raised = false;                                                                              \
+    if (!raised) {                                                                                           \
+      PIA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemvn<R, NB, UNR, EPI, NORM, AMAX>),       \
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMaxGemvnSmem))); \
+      raised = true;                                                                                         \
+    }                                                                                                        \
+    hipLaunchKernelGGL((k_gemvn<R, NB, UNR, EPI, NORM, AMAX>), grid, dim3(64 * kWaves), smem, st, w, g.ldw,  \
+                       g.scales, x, g.ldx, g.norm_w, g.eps, o, g.osb, g.osr, static_cast<int>(g.rows),        \
+                       static_cast<int>(g.cols), static_cast<int>(nb), am);                                  \
+  } while (0)
+  if constexpr (EPI == kEpiStore) {
+    if (g.amax) {
+      if (g.norm_w) PIA_GEMVN(true, true);
+      else PIA_GEMVN(false, true);
+      return;
+    }
+  }
+  if (g.norm_w) PIA_GEMVN(true, false);
+  else PIA_GEMVN(false, false);
+#undef PIA_GEMVN
+}
+
+template <int R, int NB, int UNR>
+void gon_epi(const GemvArgs& g, int64_t b0, int64_t nb, hipStream_t st) {
+  if (g.epi == Epi::Add) gon<R, NB, UNR, kEpiAdd>(g, b0, nb, st);
+  else if (g.epi == Epi::Swiglu) gon<R, NB, UNR, kEpiSwiglu>(g, b0, nb, st);
+  else gon<R, NB, UNR, kEpiStore>(g, b0, nb, st);
+}
+
+template <int NB>
+void gon_nb(const GemvArgs& g, int64_t b0, int64_t nb, hipStream_t st) {
+  // 4 rows per wavefront for tall matrices, 2 otherwise; batches of up to 4 column chunks
+  // per lane in flight (the NB accumulators per row take the registers UNR 8 would).
+  const int64_t chunks = (g.cols / 16 + 63) / 64;
+  if (g.rows >= 4 * kWaves * 512) {
+    if (chunks <= 2) gon_epi<4, NB, 2>(g, b0, nb, st);
+    else gon_epi<4, NB, 4>(g, b0, nb, st);
+  } else {
+    if (chunks <= 2) gon_epi<2, NB, 2>(g, b0, nb, st);
+    else gon_epi<2, NB, 4>(g, b0, nb, st);
+  }
+}
+
+// The batch in groups of at most 8 rows whose staged activations fit in LDS.
+void launch_gemvn(const GemvArgs& g, hipStream_t st) {
+  const int64_t row_bytes = gemvn_stride(g.cols) * 4;
+  int64_t nb_max = 8;
+  while (nb_max > 1 && nb_max * row_bytes > kMaxGemvnSmem) nb_max /= 2;
+  for (int64_t b0 = 0; b0 < g.batch; b0 += nb_max) {
+    const int64_t nb = std::min<int64_t>(nb_max, g.batch - b0);
+    if (nb <= 2) gon_nb<2>(g, b0, nb, st);
+    else if (nb <= 4) gon_nb<4>(g, b0, nb, st);
+    else gon_nb<8>(g, b0, nb, st);
+  }
+}
+
 struct Launch {
   const void* W;
   int64_t ldw;
@@ -566,6 +804,14 @@ void launch_gemv(const GemvArgs& g, hipStream_t st) {
     PIA_REQUIRE(g.scales != nullptr, "gemv: int8 weights need scales");
     if (g.rows >= 4 * kWaves * 512) go1_unr<4>(g, st);
     else go1_unr<2>(g, st);
+    PIA_HIP(hipGetLastError());
+    return;
+  }
+  if (g.wkind == 1 && g.batch > 1 && g.batch <= kMaxGemvnBatch && g.cols % 16 == 0 && g.ldw % 16 == 0 &&
+      aligned(g.W, 16) && g.ldx % 4 == 0 && aligned(g.x, 16) && (!g.norm_w || aligned(g.norm_w, 16)) &&
+      2 * gemvn_stride(g.cols) * 4 <= kMaxGemvnSmem) {
+    PIA_REQUIRE(g.scales != nullptr, "gemv: int8 weights need scales");
+    launch_gemvn(g, st);
     PIA_HIP(hipGetLastError());
     return;
   }

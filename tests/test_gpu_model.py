@@ -287,7 +287,7 @@ def test_prefix_sharing_and_cow_workload(ctx):
     gm.close()
 
 
-@pytest.mark.parametrize("batch", [1, 3, 7, 8, 13, 64, 65, 130])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 7, 8, 13, 64, 65, 130])
 def test_batched_decode_sizes(ctx, batch):
     """Decode batches on both sides of the streaming-GEMV / matrix-core switch and of the
     64-entry column tiles, ragged contexts, config-1 shapes (K = 344 exercises the padded
@@ -318,3 +318,36 @@ def test_batched_decode_sizes(ctx, batch):
     assert rel <= LOGIT_TOL
     assert am.tolist() == [orc.argmax(r) for r in lc]
     gm.close()
+
+
+@pytest.mark.parametrize("batch", [5, 12])
+def test_tinyllama_small_batch_decode(ctx, batch):
+    """TinyLlama shapes at small batches (the LDS-staged projection kernel; the down projection's
+    5632 columns split the batch into groups of 4): logits and greedy tokens vs the oracle."""
+    cfg = pia.TINYLLAMA
+    rng = np.random.default_rng(500 + batch)
+    bs = 16
+    ctxs = rng.integers(20, 300, batch)
+    need = [(int(c) + 2 + bs - 1) // bs for c in ctxs]
+    nb = sum(need)
+    perm = rng.permutation(nb).tolist()
+    tables, k = [], 0
+    for n in need:
+        tables.append(perm[k:k + n])
+        k += n
+    w = pia.synth_weights(cfg, seed=77)
+    kv = (rng.standard_normal(orc.kv_floats(cfg, nb, bs), dtype=np.float32) * 0.5)
+    gm = pia.Model(ctx, cfg, w)
+    gm.kv_alloc(nb, bs)
+    gm.kv_upload(kv)
+    om_ = orc.OracleModel(cfg, w)
+    toks = rng.integers(0, cfg.vocab, batch).tolist()
+    pos = [int(c) for c in ctxs]
+    lg, am = gm.decode(toks, pos, tables)
+    lc = om_.decode(toks, pos, tables, kv, nb, bs)
+    rel = max(_rel(lg[b], lc[b]) for b in range(batch))
+    print(f"[tinyllama batch {batch}] rel={rel:.3g}", flush=True)
+    assert rel <= LOGIT_TOL
+    assert am.tolist() == [orc.argmax(r) for r in lc]
+    gm.close()
+
