@@ -27,6 +27,8 @@ inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 constexpr int64_t kFusedNormRows = 64;
 // Batch from which int8 projections run on the matrix cores instead of the streaming GEMV.
 constexpr int64_t kMfmaMinBatch = 5;
+// 16-row tiles the decode GEMM's split-K workspace covers (255 tiles x 8 slices x 8 KiB).
+constexpr int64_t kDecSplitTiles = 255;
 
 struct Proj {
   int kind = -1;  // -1 unset, 0 f32, 1 int8
@@ -96,6 +98,8 @@ struct pia_model {
 
   int64_t cap = 0;  // rows of activation scratch
   DeviceBuffer x, xb, qkv, attn, h, logits, amax, attn_work, step, xq;
+  DeviceBuffer dec_split;  // split-K partial sums and counters of the decode GEMM
+  bool dec_split_on = true;
   int64_t mfma_min = kMfmaMinBatch;
   int64_t logit_rows = 0;  // rows of `logits` the last decode / prefill wrote
   DeviceBuffer samp;       // sampling parameters, generator states and drawn tokens
@@ -157,6 +161,10 @@ struct pia_model {
     grow(h, c * ld_i * 4);
     grow(amax, c * kArgmaxSlots * 8);
     grow(xq, xdigits_bytes(c, std::max(cfg.hidden, cfg.inter)));
+    if (!dec_split.ptr) {
+      dec_split.ensure(dec_split_bytes(kDecSplitTiles));
+      PIA_HIP(hipMemset(dec_split.ptr, 0, dec_split_bytes(kDecSplitTiles)));  // launches leave it zero
+    }
     cap = c;
   }
 
@@ -223,8 +231,11 @@ struct pia_model {
       timed(6, 0, [&] { launch_xdigits(x_in, ldx, norm_w, cfg.rms_eps, batch, p.cols, xq.ptr, st()); });
       hipEvent_t b = nullptr;
       begin(cls, proj_bytes(p, batch, epi), &b);
+      const DecSplitWork split{dec_split.as<unsigned long long>(),
+                               reinterpret_cast<unsigned*>(dec_split.as<char>() + kDecSplitTiles * 8 * 16 * 64 * 8),
+                               kDecSplitTiles};
       launch_gemm_i8_mfma(static_cast<const int8_t*>(p.w.ptr), p.ld, p.s.as<float>(), xq.ptr, out, ldo, 1, p.rows,
-                          p.cols, batch, epi, amax_out, st());
+                          p.cols, batch, epi, amax_out, dec_split_on ? &split : nullptr, st());
       end(b);
       return;
     }
@@ -594,6 +605,8 @@ pia_status pia_model_create(pia_context* ctx, const pia_model_config* cfg, pia_m
   m->layers.resize(c.layers);
   // Diagnostic override of the batch from which decode projections use the matrix cores.
   if (const char* e = std::getenv("PIA_MFMA_MIN_BATCH")) m->mfma_min = std::max<int64_t>(2, std::atoll(e));
+  // Diagnostic: PIA_DEC_SPLIT=0 turns the decode GEMM's split K off.
+  if (const char* e = std::getenv("PIA_DEC_SPLIT")) m->dec_split_on = std::atoi(e) != 0;
   *out = m;
   PIA_API_END
 }

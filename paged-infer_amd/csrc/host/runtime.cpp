@@ -341,6 +341,12 @@ pia_status pia_bench_projection(pia_context* ctx, int64_t rows, int64_t cols, in
   y.ensure(batch * rows * 4);
   nw.ensure(ldx * 4);
   xq.ensure(xdigits_bytes(batch, cols));
+  constexpr int64_t kSplitTiles = 255;
+  DeviceBuffer split_buf;
+  split_buf.ensure(dec_split_bytes(kSplitTiles));
+  PIA_HIP(hipMemset(split_buf.ptr, 0, dec_split_bytes(kSplitTiles)));
+  const DecSplitWork split{split_buf.as<unsigned long long>(),
+                           reinterpret_cast<unsigned*>(split_buf.as<char>() + kSplitTiles * 8 * 16 * 64 * 8), kSplitTiles};
   {
     std::vector<int8_t> hw(wbytes);
     for (size_t i = 0; i < hw.size(); ++i) hw[i] = static_cast<int8_t>((i * 2654435761u >> 13) % 255 - 127);
@@ -360,7 +366,8 @@ pia_status pia_bench_projection(pia_context* ctx, int64_t rows, int64_t cols, in
     const int8_t* wi = static_cast<int8_t*>(w.ptr) + (i % ncopy) * wbytes;
     if (flags & 8) {
       launch_xdigits(x.as<float>(), ldx, norm, 1e-5f, batch, cols, xq.ptr, st);
-      launch_gemm_i8_mfma(wi, ldw, s.as<float>(), xq.ptr, y.as<float>(), rows, 1, rows, cols, batch, epi, nullptr, st);
+      launch_gemm_i8_mfma(wi, ldw, s.as<float>(), xq.ptr, y.as<float>(), rows, 1, rows, cols, batch, epi, nullptr,
+                          &split, st);
     } else {
       launch_gemv(GemvArgs{1, wi, ldw, s.as<float>(), x.as<float>(), ldx, norm, 1e-5f, y.as<float>(), rows, 1, rows,
                            cols, batch, epi},

@@ -12,6 +12,8 @@
 // element) and the final conversion -- tighter than an f32 accumulation of the same dot.
 #include <cmath>
 
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -23,6 +25,10 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 // Whole 64-entry chunks from which the LDS-tiled kernel takes over (prefill sizes).
 constexpr int64_t kTileMinChunks = 4;
+constexpr int64_t kDecTargetGroups = 512;  // workgroups a split-K decode launch aims for
+constexpr int kDecMinSplitTiles = 3;        // digit column tiles (16 columns) needed to split
+constexpr int64_t kDecMinSteps = 8;        // 64-byte k-steps per slice, at least
+constexpr int64_t kDecMaxSplit = 8;
 
 __device__ inline float block_reduce_sum(float v, float* red) {
 #pragma unroll
@@ -220,13 +226,23 @@ __device__ inline uint32_t order_key(float f) {
 // Decode GEMM: one workgroup per 16 weight rows x NT*16 digit columns (all of the batch's
 // digits for NT <= 12); the 4 wavefronts split K (interleaved 64-wide steps) and their int32
 // partial sums are added in LDS. Every weight byte is read once per launch.
+//
+// Split K (gridDim.z > 1, for launches with fewer row tiles than CUs): workgroup z covers the
+// z-th slice of the k-steps and stores its exact partial sums c0 + 256 c1 + 65536 c2 in its
+// own 64-bit slots of the workspace `ws`; the last slice of a row tile to arrive adds the
+// slices in slice order (exact integers: the result does not depend on arrival order), runs
+// the epilogue and resets the tile's counter for the next launch.
 template <int NT, int EPI, bool AMAX>
 __global__ __launch_bounds__(kThreads) void k_gemm_dec(const int8_t* __restrict__ W, int64_t ldw,
                                                        const float* __restrict__ S, const int8_t* __restrict__ D,
                                                        int kpad, const float* __restrict__ pow2,
                                                        float* __restrict__ O, int64_t osb, int64_t osr, int rows,
-                                                       int batch, unsigned long long* __restrict__ amax) {
+                                                       int batch, unsigned long long* __restrict__ amax,
+                                                       unsigned long long* __restrict__ ws,
+                                                       unsigned* __restrict__ cnt) {
   __shared__ int csum[4][16][NT * 16];
+  __shared__ long long tot[16][64];
+  __shared__ int last;
   __shared__ unsigned long long best[AMAX ? 64 : 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = blockIdx.x * 16;
@@ -242,9 +258,11 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dec(const int8_t* __restrict_
   v4i acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = v4i{0, 0, 0, 0};
-  const int ksteps = kpad / 64;
+  const int nsplit = gridDim.z;
+  const int per = (kpad / 64 + nsplit - 1) / nsplit;
+  const int ks0 = blockIdx.z * per, ksteps = min(kpad / 64, ks0 + per);
   constexpr int kU = 4;  // k-steps per wave whose loads are in flight together
-  for (int s0 = wave; s0 < ksteps; s0 += 4 * kU) {
+  for (int s0 = ks0 + wave; s0 < ksteps; s0 += 4 * kU) {
     v4i a[kU];
     v4i bm[kU][NT];
 #pragma unroll
@@ -273,28 +291,59 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dec(const int8_t* __restrict_
     for (int v = 0; v < 4; ++v) csum[wave][4 * kg + v][t * 16 + r_l] = acc[t][v];
   __syncthreads();
 
-  // Epilogue: thread -> (row, batch entry); the three digit columns of b are 3b, 3b+1, 3b+2.
-  for (int idx = threadIdx.x; idx < 16 * batch; idx += kThreads) {
-    const int r = idx / batch, b = idx % batch;
-    const int row = row0 + r;
+  // This workgroup's sum for (tile row r, batch entry b); the three digit columns of b are
+  // 3b, 3b+1, 3b+2.
+  auto partial = [&](int r, int b) {
     int64_t c[3];
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
       const int col = 3 * b + j;
       c[j] = static_cast<int64_t>(csum[0][r][col]) + csum[1][r][col] + csum[2][r][col] + csum[3][r][col];
     }
-    const int64_t sum = c[0] + 256 * c[1] + 65536 * c[2];
+    return c[0] + 256 * c[1] + 65536 * c[2];
+  };
+  if (nsplit > 1) {
+    // Slot of slice z: ws[tile][z][16][64]; agent-scope stores, visible on every XCD once done.
+    const int64_t tile = static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
+    unsigned long long* wt = ws + tile * kDecMaxSplit * 16 * 64;
+    for (int idx = threadIdx.x; idx < 16 * batch; idx += kThreads) {
+      const int r = idx / batch, b = idx % batch;
+      __hip_atomic_store(wt + (static_cast<int64_t>(blockIdx.z) * 16 + r) * 64 + b,
+                         static_cast<unsigned long long>(partial(r, b)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // Waiting for the stores to complete (no cache writeback fence) orders them before the
+    // counter increment.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      unsigned* c = cnt + tile;
+      const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = old == static_cast<unsigned>(nsplit - 1);
+      if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+    for (int idx = threadIdx.x; idx < 16 * batch; idx += kThreads) {
+      const int r = idx / batch, b = idx % batch;
+      long long t = 0;
+      for (int z = 0; z < nsplit; ++z)
+        t += static_cast<long long>(__hip_atomic_load(wt + (static_cast<int64_t>(z) * 16 + r) * 64 + b,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      tot[r][b] = t;
+    }
+    __syncthreads();
+  }
+  auto total = [&](int r, int b) -> int64_t { return nsplit > 1 ? tot[r][b] : partial(r, b); };
+
+  // Epilogue: thread -> (row, batch entry).
+  for (int idx = threadIdx.x; idx < 16 * batch; idx += kThreads) {
+    const int r = idx / batch, b = idx % batch;
+    const int row = row0 + r;
+    const int64_t sum = total(r, b);
     const float y = static_cast<float>(sum) * pow2[b];
     if constexpr (EPI == kEpiSwiglu) {
       if ((r & 1) == 0 && row + 1 < rows) {
-        int64_t cu[3];
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-          const int col = 3 * b + j;
-          cu[j] = static_cast<int64_t>(csum[0][r + 1][col]) + csum[1][r + 1][col] + csum[2][r + 1][col] +
-                  csum[3][r + 1][col];
-        }
-        const float yu = static_cast<float>(cu[0] + 256 * cu[1] + 65536 * cu[2]) * pow2[b];
+        const float yu = static_cast<float>(total(r + 1, b)) * pow2[b];
         const float g = y * S[row];
         const float u = yu * S[row + 1];
         const float silu = g / (1.0f + expf(-g));
@@ -476,7 +525,7 @@ void go_rows64(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, in
 template <int NT>
 void go_dec(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, const float* pow2, float* O,
             int64_t osb, int64_t osr, int rows, int batch, int chunks, Epi epi, unsigned long long* amax,
-            hipStream_t st) {
+            const DecSplitWork* split, hipStream_t st) {
   // Tall matrices: 64-row tiles with the digits shared through LDS (enough tiles to fill the
   // CUs); short ones: 16-row tiles whose 4 wavefronts split K.
   if (static_cast<int64_t>((rows + 63) / 64) * chunks >= 96) {
@@ -487,19 +536,32 @@ void go_dec(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int k
     else go_rows64<NT, kEpiStore, false>(W, ldw, S, D, kpad, pow2, O, osb, osr, rows, batch, chunks, amax, st);
     return;
   }
-  dim3 grid((rows + 15) / 16, chunks);
+  // Split K so that a launch has about kDecTargetGroups workgroups, each slice at least
+  // kDecMinSteps k-steps long.
+  const int64_t tiles = static_cast<int64_t>((rows + 15) / 16) * chunks;
+  int nsplit = 1;
+  // Below three digit tiles (batch < 11) a workgroup's MFMA work per k-step is too small for
+  // the slice handshake to pay off.
+  if (split && split->ws && NT >= kDecMinSplitTiles && tiles <= split->max_tiles) {
+    const int64_t want = (kDecTargetGroups + tiles - 1) / tiles;
+    const int64_t cap = (kpad / 64) / kDecMinSteps;
+    nsplit = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({want, cap, kDecMaxSplit})));
+  }
+  unsigned long long* ws = nsplit > 1 ? split->ws : nullptr;
+  unsigned* cnt = nsplit > 1 ? split->cnt : nullptr;
+  dim3 grid((rows + 15) / 16, chunks, nsplit);
   if (epi == Epi::Add)
     hipLaunchKernelGGL((k_gemm_dec<NT, kEpiAdd, false>), grid, dim3(kThreads), 0, st, W, ldw, S, D, kpad, pow2, O, osb,
-                       osr, rows, batch, amax);
+                       osr, rows, batch, amax, ws, cnt);
   else if (epi == Epi::Swiglu)
     hipLaunchKernelGGL((k_gemm_dec<NT, kEpiSwiglu, false>), grid, dim3(kThreads), 0, st, W, ldw, S, D, kpad, pow2, O,
-                       osb, osr, rows, batch, amax);
+                       osb, osr, rows, batch, amax, ws, cnt);
   else if (amax)
     hipLaunchKernelGGL((k_gemm_dec<NT, kEpiStore, true>), grid, dim3(kThreads), 0, st, W, ldw, S, D, kpad, pow2, O,
-                       osb, osr, rows, batch, amax);
+                       osb, osr, rows, batch, amax, ws, cnt);
   else
     hipLaunchKernelGGL((k_gemm_dec<NT, kEpiStore, false>), grid, dim3(kThreads), 0, st, W, ldw, S, D, kpad, pow2, O,
-                       osb, osr, rows, batch, amax);
+                       osb, osr, rows, batch, amax, ws, cnt);
 }
 
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -692,9 +754,11 @@ void launch_xdigits(const float* x, int64_t ldx, const float* norm_w, float eps,
   PIA_HIP(hipGetLastError());
 }
 
+int64_t dec_split_bytes(int64_t max_tiles) { return max_tiles * kDecMaxSplit * 16 * 64 * 8 + max_tiles * 4; }
+
 void launch_gemm_i8_mfma(const int8_t* W, int64_t ldw, const float* scales, const void* xq, float* out, int64_t osb,
                          int64_t osr, int64_t rows, int64_t cols, int64_t batch, Epi epi, unsigned long long* amax,
-                         hipStream_t st) {
+                         const DecSplitWork* split, hipStream_t st) {
   const int64_t kpad = (cols + 63) / 64 * 64;
   PIA_REQUIRE(ldw >= kpad && ldw % 16 == 0, "gemm: weight rows must be padded to a multiple of 64 bytes");
   PIA_REQUIRE(scales != nullptr, "gemm: int8 weights need scales");
@@ -717,7 +781,7 @@ void launch_gemm_i8_mfma(const int8_t* W, int64_t ldw, const float* scales, cons
     switch (nt) {
 #define PIA_NT(N)                                                                                     \
   case N:                                                                                             \
-    go_dec<N>(W, ldw, scales, D, k, p2, O, osb, osr, r, nb, static_cast<int>(chunks), epi, am, st); \
+    go_dec<N>(W, ldw, scales, D, k, p2, O, osb, osr, r, nb, static_cast<int>(chunks), epi, am, split, st); \
     break;
       PIA_NT(1) PIA_NT(2) PIA_NT(3) PIA_NT(4) PIA_NT(5) PIA_NT(6) PIA_NT(7) PIA_NT(8) PIA_NT(9) PIA_NT(10)
       PIA_NT(11) PIA_NT(12)
