@@ -306,44 +306,75 @@ __global__ __launch_bounds__(256) void k_sort_keys(const float* __restrict__ log
 }
 
 struct SerialShared {
-  float buf[kSerialChunk + 8];
+  float buf[kSerialChunk + 64];  // + zero padding to whole groups + one group of over-read
   float value;
   int pos;
   int stop;
 };
 
-// Walk v[0..n) in order on one lane: f(j, v[j]) returns true to stop. Returns the index it
-// stopped at, or n. The whole workgroup stages each chunk through LDS.
-template <typename F>
-__device__ int serial_walk(const float* __restrict__ v, int n, SerialShared& sh, F&& f) {
+// One lane walks v[0..n) in order, 32 values per group, the next group's LDS reads issued
+// before this group's additions; the whole workgroup stages each chunk through LDS (zero
+// padded to a whole group: adding +0.0 leaves a non-negative running sum unchanged).
+// MODE 0: the running sum of all n values (returned in sh.value).
+// MODE 1: the first j with sum(v[0..j]) >= thr; MODE 2: the first j with thr < sum(v[0..j]).
+// The running sum never decreases (the values are >= 0), so the additions run branch-free and
+// only the group in which the sum first crosses is walked again, from the same starting value
+// (the same sequence of f32 additions). Returns that j, or n.
+template <int MODE>
+__device__ int serial_walk(const float* __restrict__ v, int n, float thr, SerialShared& sh) {
   const int tid = threadIdx.x;
+  float acc = 0.0f;  // thread 0's running sum
+  int found = n;
   for (int c0 = 0; c0 < n; c0 += kSerialChunk) {
     const int len = min(kSerialChunk, n - c0);
-    for (int j = tid; j < len; j += blockDim.x) sh.buf[j] = v[c0 + j];
+    const int padded = (len + 31) / 32 * 32;
+    for (int j = tid; j < padded; j += blockDim.x) sh.buf[j] = j < len ? v[c0 + j] : 0.0f;
     __syncthreads();
     if (tid == 0) {
       int stop = -1;
-      // Two groups of 4 in flight: the next group's LDS reads are issued before this group's
-      // dependent additions.
-      float4 cur = *reinterpret_cast<const float4*>(sh.buf);
-      int j = 0;
-      for (; j < len; j += 4) {
-        const float4 nxt = *reinterpret_cast<const float4*>(sh.buf + j + 4);
-        const float e[4] = {cur.x, cur.y, cur.z, cur.w};
+      const float4* b4 = reinterpret_cast<const float4*>(sh.buf);
+      float4 cur[8];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-          if (stop < 0 && j + u < len && f(c0 + j + u, e[u])) stop = c0 + j + u;
-        if (stop >= 0) break;
-        cur = nxt;
+      for (int q = 0; q < 8; ++q) cur[q] = b4[q];
+      for (int g = 0; g * 32 < padded; ++g) {
+        float4 nxt[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) nxt[q] = b4[(g + 1) * 8 + q];
+        const float start = acc;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          acc += cur[q].x;
+          acc += cur[q].y;
+          acc += cur[q].z;
+          acc += cur[q].w;
+        }
+        if (MODE != 0 && (MODE == 1 ? acc >= thr : thr < acc)) {
+          float c = start;
+          for (int j = 0; j < 32; ++j) {
+            c += sh.buf[g * 32 + j];
+            if (MODE == 1 ? c >= thr : thr < c) {
+              stop = c0 + g * 32 + j;
+              break;
+            }
+          }
+          break;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) cur[q] = nxt[q];
       }
       sh.stop = stop;
+      sh.value = acc;
     }
     __syncthreads();
     const int stop = sh.stop;
+    if (tid == 0) acc = sh.value;
     __syncthreads();
-    if (stop >= 0) return stop;
+    if (stop >= 0) {
+      found = stop;
+      break;
+    }
   }
-  return n;
+  return found;
 }
 
 __global__ __launch_bounds__(256) void k_sample_ordered(const float* __restrict__ logits, int64_t ld, int vocab,
@@ -388,32 +419,20 @@ __global__ __launch_bounds__(256) void k_sample_ordered(const float* __restrict_
   for (int j = tid; j < keep; j += 256)
     p[j] = static_cast<float>(exp(static_cast<double>((row[order[j]] - max_logit) * inv_temp)));
   __syncthreads();
-  float acc = 0.0f;
-  serial_walk(p, keep, sh, [&](int, float v) {
-    acc += v;
-    return false;
-  });
-  if (tid == 0) sh.value = acc;
-  __syncthreads();
+  serial_walk<0>(p, keep, 0.0f, sh);  // total: the in-order f32 sum
   const float total = sh.value;
+  __syncthreads();
   for (int j = tid; j < keep; j += 256) p[j] = p[j] / total;
   __syncthreads();
   int cut = keep;
   if (sp.top_p < 1.0f) {
-    float cum = 0.0f;
-    const int hit = serial_walk(p, keep, sh, [&](int, float v) {
-      cum += v;
-      return cum >= sp.top_p;
-    });
+    // Nucleus: the first cumulative >= top_p is the last token kept; then the renormalization.
+    const int hit = serial_walk<1>(p, keep, sp.top_p, sh);
     cut = hit < keep ? hit + 1 : keep;
-    float renorm = 0.0f;
-    serial_walk(p, cut, sh, [&](int, float v) {
-      renorm += v;
-      return false;
-    });
-    if (tid == 0) sh.value = renorm;
     __syncthreads();
+    serial_walk<0>(p, cut, 0.0f, sh);
     const float rn = sh.value;
+    __syncthreads();
     for (int j = tid; j < cut; j += 256) p[j] = p[j] / rn;
     __syncthreads();
   }
@@ -427,12 +446,7 @@ __global__ __launch_bounds__(256) void k_sample_ordered(const float* __restrict_
     draw = static_cast<float>((x * 0x2545F4914F6CDD1Dull) >> 40) / 16777216.0f;
   }
   __syncthreads();
-  const float target = draw;
-  float cum = 0.0f;
-  const int pick = serial_walk(p, cut, sh, [&](int, float v) {
-    cum += v;
-    return target < cum;
-  });
+  const int pick = serial_walk<2>(p, cut, draw, sh);
   if (tid == 0) out[r] = static_cast<int32_t>(order[pick < cut ? pick : cut - 1]);
 }
 
