@@ -139,42 +139,56 @@ __global__ __launch_bounds__(kThreads) void k_xdigits(const float* __restrict__ 
 // 64 * 4 * kV4 <= 8192 floats with cols % 4 == 0 and 16-byte aligned rows; the row is held
 // in registers between the reductions and the digit split. Longer rows keep one workgroup
 // per row (k_xdigits), which spreads them over more lanes.
-template <int kV4>
+template <int kV4, int W>
 __global__ __launch_bounds__(256) void k_xdigits_wave(const float* __restrict__ x, int64_t ldx,
                                                       const float* __restrict__ nw, float eps, int cols, int batch,
                                                       int groups, int kpad, int8_t* __restrict__ dig,
                                                       float* __restrict__ pow2) {
-  const int lane = threadIdx.x & 63;
-  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (b >= groups) return;
-  int* d0 = reinterpret_cast<int*>(dig + static_cast<int64_t>(3 * b) * kpad);
+  // W wavefronts per row (4 / W rows per workgroup); the row's lanes are sub * 64 + lane.
+  __shared__ float red[2][4];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int sub = wave % W, first = wave - sub;  // this row's first wave
+  const int rl = sub * 64 + lane;                // lane within the row
+  const int b = blockIdx.x * (4 / W) + wave / W;
+  const bool live = b < groups;
+  const bool real = b < batch;
+  int* d0 = reinterpret_cast<int*>(dig + static_cast<int64_t>(3 * (live ? b : 0)) * kpad);
   int* d1 = d0 + kpad / 4;
   int* d2 = d1 + kpad / 4;
   const int n4 = cols >> 2, kp4 = kpad >> 2;
-  if (b >= batch) {
-    for (int i = lane; i < kp4; i += 64) d0[i] = d1[i] = d2[i] = 0;
-    if (lane == 0) pow2[b] = 0.0f;
-    return;
-  }
-  const float4* x4 = reinterpret_cast<const float4*>(x + static_cast<int64_t>(b) * ldx);
+  const float4* x4 = reinterpret_cast<const float4*>(x + static_cast<int64_t>(real ? b : 0) * ldx);
   float4 v[kV4];
 #pragma unroll
   for (int u = 0; u < kV4; ++u) {
-    const int i = lane + 64 * u;
-    v[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const int i = rl + 64 * W * u;
+    v[u] = (real && i < n4) ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
+  // Row sum over the W waves: wave shuffle, then the partials through LDS.
+  auto row_reduce = [&](float t, int slot, bool is_max) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float o = __shfl_xor(t, off, 64);
+      t = is_max ? fmaxf(t, o) : t + o;
+    }
+    if (W == 1) return t;
+    if (lane == 0) red[slot][wave] = t;
+    __syncthreads();
+    float r = red[slot][first];
+#pragma unroll
+    for (int w = 1; w < W; ++w) r = is_max ? fmaxf(r, red[slot][first + w]) : r + red[slot][first + w];
+    return r;
+  };
   if (nw) {
     const float4* w4 = reinterpret_cast<const float4*>(nw);
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < kV4; ++u) ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    ss = row_reduce(ss, 0, false);
     const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
 #pragma unroll
     for (int u = 0; u < kV4; ++u) {
-      const int i = lane + 64 * u;
-      if (i < n4) {
+      const int i = rl + 64 * W * u;
+      if (real && i < n4) {
         const float4 w = w4[i];
         v[u] = make_float4((v[u].x * inv) * w.x, (v[u].y * inv) * w.y, (v[u].z * inv) * w.z, (v[u].w * inv) * w.w);
       }
@@ -183,8 +197,8 @@ __global__ __launch_bounds__(256) void k_xdigits_wave(const float* __restrict__ 
   float m = 0.0f;
 #pragma unroll
   for (int u = 0; u < kV4; ++u) m = fmaxf(m, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  m = row_reduce(m, 1, true);
+  if (!live) return;
   int e = 0;
   if (m > 0.0f) (void)frexpf(m, &e);  // m = f * 2^e, f in [0.5, 1): max|x| < 2^e
   const int sh = 22 - e;
@@ -198,9 +212,10 @@ __global__ __launch_bounds__(256) void k_xdigits_wave(const float* __restrict__ 
   auto pack = [](int a, int b_, int c, int d) {
     return (a & 255) | ((b_ & 255) << 8) | ((c & 255) << 16) | (d << 24);
   };
+  // Rows past the batch (zero digits) have v == 0 and m == 0: every digit is 0.
 #pragma unroll
   for (int u = 0; u < kV4; ++u) {
-    const int i = lane + 64 * u;
+    const int i = rl + 64 * W * u;
     if (i < n4) {
       int a[4], bb[4], c[4];
       split(v[u].x, a[0], bb[0], c[0]);
@@ -212,8 +227,8 @@ __global__ __launch_bounds__(256) void k_xdigits_wave(const float* __restrict__ 
       d2[i] = pack(c[0], c[1], c[2], c[3]);
     }
   }
-  for (int i = n4 + lane; i < kp4; i += 64) d0[i] = d1[i] = d2[i] = 0;  // the k-step padding
-  if (lane == 0) pow2[b] = ldexpf(1.0f, -sh);
+  for (int i = n4 + rl; i < kp4; i += 64 * W) d0[i] = d1[i] = d2[i] = 0;  // the k-step padding
+  if (rl == 0) pow2[b] = real ? ldexpf(1.0f, -sh) : 0.0f;
 }
 
 enum { kEpiStore = 0, kEpiAdd = 1, kEpiSwiglu = 2 };
@@ -737,15 +752,17 @@ void launch_xdigits(const float* x, int64_t ldx, const float* norm_w, float eps,
   const bool vec = cols % 4 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
                    (!norm_w || (reinterpret_cast<uintptr_t>(norm_w) & 15) == 0);
   const int64_t v4 = (cols / 4 + 63) / 64;  // float4 per lane
-  if (vec && v4 <= 32) {
-    const dim3 grid(static_cast<unsigned>((groups + 3) / 4));
-#define PIA_XDW(V)                                                                                            \
-  hipLaunchKernelGGL(k_xdigits_wave<V>, grid, dim3(256), 0, st, x, ldx, norm_w, eps, static_cast<int>(cols), \
-                     static_cast<int>(batch), static_cast<int>(groups), static_cast<int>(kpad), dig, pow2)
-    if (v4 <= 8) PIA_XDW(8);
-    else if (v4 <= 16) PIA_XDW(16);
-    else if (v4 <= 24) PIA_XDW(24);
-    else PIA_XDW(32);
+  if (vec && v4 <= 64) {
+    // One wavefront per row up to 2048 floats, two up to 4096, four beyond (at most 16
+    // float4 per lane in registers).
+#define PIA_XDW(V, W)                                                                                            \
+  hipLaunchKernelGGL((k_xdigits_wave<V, W>), dim3(static_cast<unsigned>((groups + 4 / W - 1) / (4 / W))), dim3(256), \
+                     0, st, x, ldx, norm_w, eps, static_cast<int>(cols), static_cast<int>(batch),                 \
+                     static_cast<int>(groups), static_cast<int>(kpad), dig, pow2)
+    if (v4 <= 8) PIA_XDW(8, 1);
+    else if (v4 <= 16) PIA_XDW(8, 2);
+    else if (v4 <= 32) PIA_XDW(8, 4);
+    else PIA_XDW(16, 4);
 #undef PIA_XDW
   } else {
     hipLaunchKernelGGL(k_xdigits, dim3(static_cast<unsigned>(groups)), dim3(kThreads), 0, st, x, ldx, norm_w, eps,
