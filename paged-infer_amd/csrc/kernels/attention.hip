@@ -62,7 +62,7 @@ struct AttnParams {
 // (online) softmax: per chunk the new maximum rescales the running sum and the V accumulators.
 template <int G, int HD, int TPT, bool FUSED>
 __global__ __launch_bounds__(kThreads) void k_attn(AttnParams p) {
-  extern __shared__ float smem[];
+  extern __shared__ __align__(16) float smem[];
   const int hd = HD ? HD : p.hd;
   constexpr int kChunk = kThreads / TPT;                    // tokens per chunk
   float* qs = smem;                                         // [G][hd]

@@ -572,7 +572,7 @@ __device__ void attn_item(const StepParams& p, int layer, int kvh, int s, int S,
 
 template <int HD>
 __global__ __launch_bounds__(kThreads) void k_decode_step(StepParams p) {
-  extern __shared__ float lds[];
+  extern __shared__ __align__(16) float lds[];
   __shared__ float red[kWaves];
   __shared__ int abort_flag;
   const int lane = threadIdx.x & 63;

@@ -405,7 +405,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_rows64(const int8_t* __restri
                                                           int batch, unsigned long long* __restrict__ amax) {
   using T = Rows64<NT>;
   constexpr int kN = T::kN, kKC = T::kKC, kPitch = T::kPitch, kDig = T::kDig, kU = kKC / 64;
-  extern __shared__ int8_t lds[];  // [2][kN][kPitch] digits; reused as int32 C [64][kN]
+  extern __shared__ __align__(16) int8_t lds[];  // [2][kN][kPitch] digits; reused as int32 C [64][kN]
   __shared__ unsigned long long best[AMAX ? 64 : 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = blockIdx.x * 64;
@@ -600,7 +600,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const int8_t* __restrict
                                                         int kpad, const float* __restrict__ pow2,
                                                         float* __restrict__ O, int64_t osb, int64_t osr, int rows) {
   using namespace tile;
-  extern __shared__ int8_t lds[];
+  extern __shared__ __align__(16) int8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row0 = blockIdx.x * kBM;
   const int col0 = blockIdx.y * kBN;  // digit rows of D; batch entries 64 * blockIdx.y ..

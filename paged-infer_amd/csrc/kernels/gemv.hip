@@ -287,7 +287,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv1(const int8_t* __restrict_
                                                        const float* __restrict__ NW, float eps, float* __restrict__ O,
                                                        int64_t osr, int rows, int cols,
                                                        unsigned long long* __restrict__ amax) {
-  extern __shared__ float xs[];
+  extern __shared__ __align__(16) float xs[];
   __shared__ float red[kWaves];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * kWaves + wave) * R;
@@ -497,7 +497,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemvn(const int8_t* __restrict_
                                                        int64_t ldx, const float* __restrict__ NW, float eps,
                                                        float* __restrict__ O, int64_t osb, int64_t osr, int rows,
                                                        int cols, int batch, unsigned long long* __restrict__ amax) {
-  extern __shared__ float xs[];
+  extern __shared__ __align__(16) float xs[];
   __shared__ float red[NB][kWaves];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * kWaves + wave) * R;
