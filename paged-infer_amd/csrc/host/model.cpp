@@ -988,17 +988,33 @@ pia_status pia_model_sample(pia_model* m, const pia_sampling* params, uint64_t* 
                 "sample: NaN temperature or top_p");
   }
   PIA_HIP(hipSetDevice(m->ctx->device));
+  // One upload of [params][states] and one download of [states][tokens] through pinned staging
+  // (the previous decode's uploads from it finished before that call returned).
   const size_t pb = static_cast<size_t>(n) * sizeof(pia_sampling), rb = static_cast<size_t>(n) * 8;
-  m->grow(m->samp, pb + rb + static_cast<size_t>(n) * 4);
+  const size_t ob = static_cast<size_t>(n) * 4;
+  m->grow(m->samp, pb + rb + ob);
+  m->pin.ensure(pb + rb);
+  m->pin_out.ensure(rb + ob);
+  std::memcpy(m->pin.ptr, params, pb);
+  std::memcpy(static_cast<char*>(m->pin.ptr) + pb, rng_state, rb);
   char* d = static_cast<char*>(m->samp.ptr);
-  PIA_HIP(hipMemcpyAsync(d, params, pb, hipMemcpyHostToDevice, m->st()));
-  PIA_HIP(hipMemcpyAsync(d + pb, rng_state, rb, hipMemcpyHostToDevice, m->st()));
-  sample_with_context(m->ctx, reinterpret_cast<int32_t*>(d + pb + rb), m->logits.as<float>(), m->ld_v, n,
-                      m->cfg.vocab, reinterpret_cast<const pia_sampling*>(d), reinterpret_cast<uint64_t*>(d + pb), mode,
-                      m->st());
-  PIA_HIP(hipMemcpyAsync(rng_state, d + pb, rb, hipMemcpyDeviceToHost, m->st()));
-  PIA_HIP(hipMemcpyAsync(out, d + pb + rb, static_cast<size_t>(n) * 4, hipMemcpyDeviceToHost, m->st()));
+  PIA_HIP(hipMemcpyAsync(d, m->pin.ptr, pb + rb, hipMemcpyHostToDevice, m->st()));
+  // Every row greedy or with a small top-k: no sort of the vocabulary is needed, and the result
+  // is the reference's in either mode.
+  bool small_k = true;
+  for (int64_t i = 0; i < n; ++i)
+    small_k = small_k && (!(params[i].temperature > 0.0f) || (params[i].top_k > 0 && params[i].top_k <= sample_topk_max()));
+  if (small_k)
+    launch_sample_topk(m->logits.as<float>(), m->ld_v, n, m->cfg.vocab, reinterpret_cast<const pia_sampling*>(d),
+                       reinterpret_cast<uint64_t*>(d + pb), reinterpret_cast<int32_t*>(d + pb + rb), m->st());
+  else
+    sample_with_context(m->ctx, reinterpret_cast<int32_t*>(d + pb + rb), m->logits.as<float>(), m->ld_v, n,
+                        m->cfg.vocab, reinterpret_cast<const pia_sampling*>(d), reinterpret_cast<uint64_t*>(d + pb),
+                        mode, m->st());
+  PIA_HIP(hipMemcpyAsync(m->pin_out.ptr, d + pb, rb + ob, hipMemcpyDeviceToHost, m->st()));
   PIA_HIP(hipStreamSynchronize(m->st()));
+  std::memcpy(rng_state, m->pin_out.ptr, rb);
+  std::memcpy(out, static_cast<char*>(m->pin_out.ptr) + rb, ob);
   PIA_API_END
 }
 

@@ -127,6 +127,11 @@ void launch_quantize_rows(const float* w, int64_t rows, int64_t cols, int8_t* q,
 // device sort, then in-order f32 sums; needs sample_workspace_bytes(n, vocab) of workspace);
 // mode 1: radix search with exact fixed-point sums (no workspace).
 size_t sample_workspace_bytes(int64_t n, int64_t vocab);
+// Rows whose temperature is <= 0 or whose top_k is in 1..sample_topk_max(): the reference's
+// order without a sort of the vocabulary (the kept tokens are selected, then sorted in LDS).
+int64_t sample_topk_max();
+void launch_sample_topk(const float* logits, int64_t ld, int64_t n, int64_t vocab, const pia_sampling* params,
+                        uint64_t* rng, int32_t* out, hipStream_t st);
 void launch_sample(const float* logits, int64_t ld, int64_t n, int64_t vocab, const pia_sampling* params,
                    uint64_t* rng, int32_t* out, int mode, void* workspace, size_t workspace_bytes, hipStream_t st);
 

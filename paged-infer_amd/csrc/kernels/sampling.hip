@@ -92,13 +92,45 @@ struct Ctx {
   Rank keep_p;  // nucleus bound
 };
 
+// f(i, logit) for every token of the row in thread-strided order, eight loads in flight per
+// thread (a runtime-bounded loop would otherwise wait for one load per iteration).
+template <typename F>
+__device__ inline void for_each_strided(const float* __restrict__ row, int vocab, F&& f) {
+  for (int i0 = threadIdx.x; i0 < vocab; i0 += 8 * kThreads) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * kThreads;
+      v[u] = i < vocab ? row[i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * kThreads;
+      if (i < vocab) f(i, v[u]);
+    }
+  }
+}
+
+// f(i, logit) for tokens i0..i1-1 in order, eight loads in flight.
+template <typename F>
+__device__ inline void for_each_range(const float* __restrict__ row, int i0, int i1, F&& f) {
+  for (int b = i0; b < i1; b += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = b + u < i1 ? row[b + u] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (b + u < i1) f(b + u, v[u]);
+  }
+}
+
 // Weight of token i (key k) for a search: 1 per token (count) or its fixed-point probability
 // weight, 0 outside the kept set.
 template <bool MASS>
-__device__ inline unsigned long long weight(const Ctx& c, int i, uint32_t k) {
+__device__ inline unsigned long long weight(const Ctx& c, int i, uint32_t k, float logit) {
   if (!at_or_before(k, i, c.keep_k) || !at_or_before(k, i, c.keep_p)) return 0;
   if (!MASS) return 1;
-  const float e = expf((c.row[i] - c.max_logit) * c.inv_temp);
+  const float e = expf((logit - c.max_logit) * c.inv_temp);
   return static_cast<unsigned long long>(static_cast<double>(e) * kFix);
 }
 
@@ -117,18 +149,18 @@ __device__ Rank find_crossing(const Ctx& c, unsigned long long thr, Shared& sh, 
     // tokens in a few bins): merge runs in registers before touching LDS.
     int run_d = -1;
     unsigned long long run_w = 0;
-    for (int i = tid; i < c.vocab; i += kThreads) {
-      const uint32_t k = order_key(c.row[i]);
-      if ((k & mask) != prefix) continue;
-      const unsigned long long w = weight<MASS>(c, i, k);
-      if (!w) continue;
+    for_each_strided(c.row, c.vocab, [&](int i, float logit) {
+      const uint32_t k = order_key(logit);
+      if ((k & mask) != prefix) return;
+      const unsigned long long w = weight<MASS>(c, i, k, logit);
+      if (!w) return;
       const int d = (k >> shift) & 255;
       if (d != run_d) {
         if (run_w) atomicAdd(&sh.hist[run_d], run_w);
         run_d = d, run_w = 0;
       }
       run_w += w;
-    }
+    });
     if (run_w) atomicAdd(&sh.hist[run_d], run_w);
     __syncthreads();
     // Wave 0: lane l owns digits 255-4l .. 252-4l (descending); an inclusive scan over lanes
@@ -177,10 +209,10 @@ __device__ Rank find_crossing(const Ctx& c, unsigned long long thr, Shared& sh, 
   const int chunk = (c.vocab + kThreads - 1) / kThreads;
   const int i0 = tid * chunk, i1 = min(c.vocab, i0 + chunk);
   unsigned long long local = 0;
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t k = order_key(c.row[i]);
-    if (k == prefix) local += weight<MASS>(c, i, k);
-  }
+  for_each_range(c.row, i0, i1, [&](int i, float logit) {
+    const uint32_t k = order_key(logit);
+    if (k == prefix) local += weight<MASS>(c, i, k, logit);
+  });
   if (tid == 0) sh.found_idx = -1, sh.found_cum = 0;
   sh.scan[tid] = local;
   __syncthreads();
@@ -195,9 +227,10 @@ __device__ Rank find_crossing(const Ctx& c, unsigned long long thr, Shared& sh, 
   if (local && excl < thr && excl + local >= thr) {
     unsigned long long b = excl;
     for (int i = i0; i < i1; ++i) {
-      const uint32_t k = order_key(c.row[i]);
+      const float logit = c.row[i];
+      const uint32_t k = order_key(logit);
       if (k != prefix) continue;
-      b += weight<MASS>(c, i, k);
+      b += weight<MASS>(c, i, k, logit);
       if (b >= thr) {
         sh.found_idx = i;
         sh.found_cum = b;
@@ -228,10 +261,10 @@ __global__ __launch_bounds__(kThreads) void k_sample(const float* __restrict__ l
   // temperature <= 0 the answer is argmax, the last of equal maxima (src/sampling.rs:140-147).
   uint32_t kmax = 0;
   int imax = -1;
-  for (int i = tid; i < vocab; i += kThreads) {
-    const uint32_t k = order_key(c.row[i]);
+  for_each_strided(c.row, vocab, [&](int i, float logit) {
+    const uint32_t k = order_key(logit);
     if (imax < 0 || k > kmax || (k == kmax && i > imax)) kmax = k, imax = i;
-  }
+  });
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const uint32_t ok = __shfl_xor(kmax, off, 64);
@@ -257,7 +290,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(const float* __restrict__ l
 
   // Total weight of the kept tokens.
   unsigned long long local = 0;
-  for (int i = tid; i < vocab; i += kThreads) local += weight<true>(c, i, order_key(c.row[i]));
+  for_each_strided(c.row, vocab, [&](int i, float logit) { local += weight<true>(c, i, order_key(logit), logit); });
   unsigned long long total = block_sum_u64(local, sh);
 
   // Nucleus: the first token whose cumulative share reaches top_p is the last one kept.
@@ -450,6 +483,152 @@ __global__ __launch_bounds__(256) void k_sample_ordered(const float* __restrict_
   if (tid == 0) out[r] = static_cast<int32_t>(order[pick < cut ? pick : cut - 1]);
 }
 
+// ---------------------------------------------------------------------------------------
+// Small top-k, reference order, no sort of the vocabulary.
+// ---------------------------------------------------------------------------------------
+constexpr int kTopkMax = 1024;
+constexpr int kTopkLdsVocab = 32768;  // rows up to this many logits are staged in LDS
+
+// Rows with temperature <= 0 (argmax) or 0 < top_k <= kTopkMax: the radix search finds the
+// k-th token of the ranking, the kept tokens are gathered into LDS and bitonic-sorted there by
+// (logit total order descending, index ascending), and one lane runs the reference's in-order
+// arithmetic over at most kTopkMax values (the same operations as k_sample_ordered).
+__global__ __launch_bounds__(kThreads) void k_sample_topk(const float* __restrict__ logits, int64_t ld, int vocab,
+                                                          const pia_sampling* __restrict__ params,
+                                                          uint64_t* __restrict__ rng, int32_t* __restrict__ out) {
+  extern __shared__ __align__(16) float lrow[];  // the row's logits, when they fit (vocab <= kTopkLdsVocab)
+  __shared__ Shared sh;
+  __shared__ unsigned long long sk[kTopkMax];  // (~key << 32 | index): ascending = ranking order
+  __shared__ float pr[kTopkMax];
+  __shared__ int count;
+  __shared__ float bval;
+  __shared__ int bpos;
+  const int e = blockIdx.x, tid = threadIdx.x;
+  const pia_sampling sp = params[e];
+  Ctx c;
+  c.row = logits + static_cast<int64_t>(e) * ld;
+  c.vocab = vocab;
+  c.keep_k = Rank{0, -1};
+  c.keep_p = Rank{0, -1};
+  if (!(sp.temperature > 0.0f)) {
+    uint32_t kmax = 0;
+    int imax = -1;
+    for_each_strided(c.row, vocab, [&](int i, float logit) {
+      const uint32_t k = order_key(logit);
+      if (imax < 0 || k > kmax || (k == kmax && i > imax)) kmax = k, imax = i;
+    });
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const uint32_t ok = __shfl_xor(kmax, off, 64);
+      const int oi = __shfl_xor(imax, off, 64);
+      if (oi >= 0 && (imax < 0 || ok > kmax || (ok == kmax && oi > imax))) kmax = ok, imax = oi;
+    }
+    __shared__ uint32_t wk[kWaves];
+    __shared__ int32_t wi[kWaves];
+    if ((tid & 63) == 0) wk[tid >> 6] = kmax, wi[tid >> 6] = imax;
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 0; w < kWaves; ++w)
+        if (wi[w] >= 0 && (imax < 0 || wk[w] > kmax || (wk[w] == kmax && wi[w] > imax))) kmax = wk[w], imax = wi[w];
+      out[e] = imax;
+    }
+    return;
+  }
+  const int keep = min(sp.top_k, vocab);
+  // Every later pass reads the row from LDS when it fits.
+  if (vocab <= kTopkLdsVocab) {
+    for_each_strided(c.row, vocab, [&](int i, float logit) { lrow[i] = logit; });
+    __syncthreads();
+    c.row = lrow;
+  }
+  // The keep-th token of the ranking, then every token at or before it.
+  unsigned long long cum = 0;
+  const Rank bound = keep < vocab ? find_crossing<false>(c, static_cast<unsigned long long>(keep), sh, &cum) : Rank{0, -1};
+  if (tid == 0) count = 0;
+  int n2 = 1;
+  while (n2 < keep) n2 <<= 1;
+  for (int j = tid; j < n2; j += kThreads) sk[j] = ~0ull;
+  __syncthreads();
+  for_each_strided(c.row, vocab, [&](int i, float logit) {
+    const uint32_t k = order_key(logit);
+    if (at_or_before(k, i, bound)) {
+      const int slot = atomicAdd(&count, 1);
+      if (slot < kTopkMax) sk[slot] = (static_cast<unsigned long long>(~k) << 32) | static_cast<uint32_t>(i);
+    }
+  });
+  __syncthreads();
+  // Bitonic sort of n2 entries, ascending.
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int j = tid; j < n2; j += kThreads) {
+        const int o = j ^ stride;
+        if (o > j) {
+          const bool up = (j & size) == 0;
+          const unsigned long long a = sk[j], b = sk[o];
+          if ((a > b) == up) sk[j] = b, sk[o] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // The reference's arithmetic over the kept tokens in ranking order (src/sampling.rs:95-136).
+  const float inv_temp = 1.0f / sp.temperature;
+  const float max_logit = c.row[static_cast<uint32_t>(sk[0])];
+  for (int j = tid; j < keep; j += kThreads)
+    pr[j] = static_cast<float>(exp(static_cast<double>((c.row[static_cast<uint32_t>(sk[j])] - max_logit) * inv_temp)));
+  __syncthreads();
+  if (tid == 0) {
+    float total = 0.0f;
+    for (int j = 0; j < keep; ++j) total += pr[j];
+    bval = total;
+  }
+  __syncthreads();
+  const float total = bval;
+  for (int j = tid; j < keep; j += kThreads) pr[j] = pr[j] / total;
+  __syncthreads();
+  int cut = keep;
+  if (sp.top_p < 1.0f) {
+    if (tid == 0) {
+      float cumulative = 0.0f;
+      int cc = keep;
+      for (int j = 0; j < keep; ++j) {
+        cumulative += pr[j];
+        if (cumulative >= sp.top_p) {
+          cc = j + 1;
+          break;
+        }
+      }
+      float renorm = 0.0f;
+      for (int j = 0; j < cc; ++j) renorm += pr[j];
+      bpos = cc;
+      bval = renorm;
+    }
+    __syncthreads();
+    cut = bpos;
+    const float rn = bval;
+    for (int j = tid; j < cut; j += kThreads) pr[j] = pr[j] / rn;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    uint64_t x = rng[e];
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    rng[e] = x;
+    const float target = static_cast<float>((x * 0x2545F4914F6CDD1Dull) >> 40) / 16777216.0f;
+    float cumulative = 0.0f;
+    int pick = cut - 1;
+    for (int j = 0; j < cut; ++j) {
+      cumulative += pr[j];
+      if (target < cumulative) {
+        pick = j;
+        break;
+      }
+    }
+    out[e] = static_cast<int32_t>(static_cast<uint32_t>(sk[pick]));
+  }
+}
+
 }  // namespace
 
 size_t sample_workspace_bytes(int64_t n, int64_t vocab) {
@@ -462,6 +641,24 @@ size_t sample_workspace_bytes(int64_t n, int64_t vocab) {
   auto up = [](size_t b) { return (b + 255) / 256 * 256; };
   return 2 * up(N * 8) + 2 * up(N * 4) + up(N * 4) + up(temp);
 }
+
+void launch_sample_topk(const float* logits, int64_t ld, int64_t n, int64_t vocab, const pia_sampling* params,
+                        uint64_t* rng, int32_t* out, hipStream_t st) {
+  if (n == 0) return;
+  PIA_REQUIRE(vocab > 0 && vocab < (int64_t(1) << 31) && ld >= vocab, "sample: bad vocabulary / pitch");
+  const size_t smem = vocab <= kTopkLdsVocab ? static_cast<size_t>(vocab) * 4 : 0;
+  static bool raised = false;
+  if (!raised) {
+    PIA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_sample_topk), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                kTopkLdsVocab * 4));
+    raised = true;
+  }
+  hipLaunchKernelGGL(k_sample_topk, dim3(static_cast<unsigned>(n)), dim3(kThreads), smem, st, logits, ld,
+                     static_cast<int>(vocab), params, rng, out);
+  PIA_HIP(hipGetLastError());
+}
+
+int64_t sample_topk_max() { return kTopkMax; }
 
 void launch_sample(const float* logits, int64_t ld, int64_t n, int64_t vocab, const pia_sampling* params,
                    uint64_t* rng, int32_t* out, int mode, void* workspace, size_t workspace_bytes, hipStream_t st) {

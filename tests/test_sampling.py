@@ -275,3 +275,28 @@ def test_model_sample_after_decode(ctx):
     assert a == b
     assert run(18) != a
     gm.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("vocab", [512, 32000])
+def test_model_sample_small_topk_path(ctx, vocab):
+    """Every row greedy or with top_k <= 1024: pia_model_sample selects and sorts only the kept
+    tokens (no sort of the vocabulary) and must still give the oracle sampler's token exactly,
+    with the same generator states."""
+    cfg = pia.LlamaConfig(hidden=128, layers=1, heads=4, kv_heads=2, inter=256, vocab=vocab)
+    w = pia.synth_weights(cfg, seed=9, std=0.2)
+    gm = pia.Model(ctx, cfg, w)
+    gm.kv_alloc(16, 16)
+    params = [(0.7, 1.0, 1), (1.3, 0.9, 40), (0.9, 0.3, 5), (1.0, 1.0, 1024), (0.0, 1.0, 0), (2.0, 0.95, vocab if vocab <= 1024 else 300)]
+    n = len(params)
+    tables = [[2 * i, 2 * i + 1] for i in range(n)]
+    states = np.array([pia.rng_new(100 + i) for i in range(n)], np.uint64)
+    samplers = [orc.Sampler(*params[i], 100 + i) for i in range(n)]
+    toks = list(range(3, 3 + n))
+    for pos in range(12):
+        lg, _ = gm.decode(toks, [pos] * n, tables)
+        toks = gm.sample(params, states)
+        want = [samplers[i].sample(lg[i]) for i in range(n)]
+        assert toks == want, (pos, toks, want)
+    assert [int(s) for s in states] == [s.rng.state.value for s in samplers]
+    gm.close()
