@@ -300,6 +300,12 @@ __global__ __launch_bounds__(kMaxHd) void k_attn_combine(const float* __restrict
   const int e = eh / heads, h = eh % heads;
   const int t = threadIdx.x;
   const float* ml = part_ml + static_cast<int64_t>(eh) * nsplit * 2;
+  // The first kPre splits' outputs do not depend on the maxima: their loads go out with them.
+  constexpr int kPre = 16;
+  const float* po = part_o + static_cast<int64_t>(eh) * nsplit * hd + t;
+  float pv[kPre];
+#pragma unroll
+  for (int u = 0; u < kPre; ++u) pv[u] = (t < hd && u < nsplit) ? po[static_cast<int64_t>(u) * hd] : 0.0f;
   // nsplit <= 128 = blockDim: thread k owns split k.
   const float mk = t < nsplit ? ml[2 * t] : -INFINITY;
   const float lk = t < nsplit ? ml[2 * t + 1] : 0.0f;
@@ -321,9 +327,11 @@ __global__ __launch_bounds__(kMaxHd) void k_attn_combine(const float* __restrict
   if (t == 0) lsum = lw[0] + lw[1];
   __syncthreads();
   if (t >= hd) return;
-  const float* po = part_o + static_cast<int64_t>(eh) * nsplit * hd + t;
   float acc = 0.0f;
-  int k = 0;
+#pragma unroll
+  for (int u = 0; u < kPre; ++u)
+    if (u < nsplit) acc = __builtin_fmaf(pv[u], w[u], acc);
+  int k = kPre;
   for (; k + 8 <= nsplit; k += 8) {
     float v[8];
 #pragma unroll
