@@ -91,6 +91,7 @@ constexpr int kWaves = 4;  // wavefronts per workgroup
 constexpr int64_t kMaxStagedCols = 16384;  // batch-1 vectors up to this length are staged in LDS
 constexpr int kMaxNormBatch = 64;
 constexpr int64_t kMaxGemvnBatch = 4;  // batches up to this size take the LDS-staged kernel
+static_assert(kMaxGemvnBatch <= 4, "launch_gemvn instantiates groups of up to 4 rows");
 
 enum { kEpiStore = 0, kEpiAdd = 1, kEpiSwiglu = 2 };
 
@@ -703,16 +704,16 @@ void gon_nb(const GemvArgs& g, int64_t b0, int64_t nb, hipStream_t st) {
   }
 }
 
-// The batch in groups of at most 8 rows whose staged activations fit in LDS.
+// The batch (at most kMaxGemvnBatch rows) in groups of at most 4 rows whose staged activations
+// fit in LDS.
 void launch_gemvn(const GemvArgs& g, hipStream_t st) {
   const int64_t row_bytes = gemvn_stride(g.cols) * 4;
-  int64_t nb_max = 8;
+  int64_t nb_max = 4;
   while (nb_max > 1 && nb_max * row_bytes > kMaxGemvnSmem) nb_max /= 2;
   for (int64_t b0 = 0; b0 < g.batch; b0 += nb_max) {
     const int64_t nb = std::min<int64_t>(nb_max, g.batch - b0);
     if (nb <= 2) gon_nb<2>(g, b0, nb, st);
-    else if (nb <= 4) gon_nb<4>(g, b0, nb, st);
-    else gon_nb<8>(g, b0, nb, st);
+    else gon_nb<4>(g, b0, nb, st);
   }
 }
 
