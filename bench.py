@@ -503,7 +503,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the int8 decode path is built and measured on a single MI355X; "
-              "multi-GPU sharding is design-only (DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "multi-GPU sharding is not built (every box has one GPU). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if args.no_cpu:
         os.environ["BENCH_CPU"] = "0"
