@@ -300,3 +300,33 @@ def test_model_sample_small_topk_path(ctx, vocab):
         assert toks == want, (pos, toks, want)
     assert [int(s) for s in states] == [s.rng.state.value for s in samplers]
     gm.close()
+
+
+@pytest.mark.gpu
+def test_sampling_argument_errors(ctx):
+    cfg = pia.LlamaConfig(hidden=128, layers=1, heads=4, kv_heads=2, inter=256, vocab=64)
+    gm = pia.Model(ctx, cfg, pia.synth_weights(cfg, seed=3))
+    gm.kv_alloc(4, 16)
+    gm.decode([1, 2], [0, 0], [[0], [1]])
+    st = np.array([pia.rng_new(1), pia.rng_new(2)], np.uint64)
+    with pytest.raises(pia.PiaError, match="NaN"):
+        gm.sample([(float("nan"), 1.0, 0), (1.0, 1.0, 0)], st)
+    with pytest.raises(pia.PiaError, match="bad sampling parameters"):
+        gm.sample([(1.0, 1.0, -1), (1.0, 1.0, 0)], st)
+    a = pia.sampling_array([(1.0, 1.0, 0), (1.0, 1.0, 0)])
+    a["reserved"][0] = 7
+    out = np.zeros(2, np.int32)
+    with pytest.raises(pia.PiaError, match="bad sampling parameters"):
+        pia.check(pia.lib().pia_model_sample(gm.h, pia.ptr(a), pia.ptr(st), 2, 0, pia.ptr(out)))
+    st3 = np.array([pia.rng_new(i) for i in range(3)], np.uint64)
+    with pytest.raises(pia.PiaError, match="no logits for that many rows"):
+        gm.sample([(1.0, 1.0, 0)] * 3, st3)
+    dl = ctx.to_device(np.zeros((1, 64), np.float32))
+    dp = ctx.to_device(pia.sampling_array([(1.0, 1.0, 0)]))
+    dr = ctx.to_device(np.array([pia.rng_new(0)], np.uint64))
+    do = ctx.empty((1,), np.int32)
+    with pytest.raises(pia.PiaError, match="unknown sampling mode"):
+        pia.check(pia.lib().pia_sample_dev(ctx.h, do.ptr, dl.ptr, 64, 1, 64, dp.ptr, dr.ptr, 5, None))
+    for d in (dl, dp, dr, do):
+        d.free()
+    gm.close()

@@ -236,3 +236,16 @@ def test_speculation_reduces_passes_and_keeps_accounting(ctx):
         out, _, _ = _generate(m, [_repetitive(tokens)], max_tokens, 4)
         assert len(out[0]) == max_tokens
     m.close()
+
+
+@pytest.mark.gpu
+def test_verify_groups_argument_errors(ctx):
+    cfg = pia.LlamaConfig(hidden=128, layers=1, heads=4, kv_heads=2, inter=256, vocab=64)
+    gm = pia.Model(ctx, cfg, pia.synth_weights(cfg, seed=3))
+    gm.kv_alloc(4, 16)
+    with pytest.raises(pia.PiaError, match="at least its held token"):
+        gm.verify_groups([(0, [], [0])])
+    with pytest.raises(pia.PiaError, match="block table entry out of range"):
+        gm.verify_groups([(0, [1, 2], [9])])
+    assert gm.verify_groups([]) == ([], [], [], 0)
+    gm.close()
