@@ -25,7 +25,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 // Whole 64-entry chunks from which the LDS-tiled kernel takes over (prefill sizes).
 constexpr int64_t kTileMinChunks = 4;
-constexpr int64_t kDecTargetGroups = 512;  // workgroups a split-K decode launch aims for
+// Workgroups a split-K decode launch aims for (batch 32: 256 beat 512, and 512 beat 1024).
+constexpr int64_t kDecTargetGroups = 256;
 constexpr int kDecMinSplitTiles = 3;        // digit column tiles (16 columns) needed to split
 constexpr int64_t kDecMinSteps = 8;        // 64-byte k-steps per slice, at least
 constexpr int64_t kDecMaxSplit = 8;
