@@ -91,6 +91,9 @@ pia_status pia_matmat_i8_dev(pia_context* ctx, float* out_rb, const float* x_br,
  * followed by transpose_rb_to_br, fused. */
 pia_status pia_qlinear_apply_dev(pia_context* ctx, float* out_br, const float* x_br, const int8_t* w,
                                  const float* scales, int64_t batch, int64_t rows, int64_t cols, void* stream);
+/* Host-pointer form of the above (same reference function), synchronous. */
+pia_status pia_qlinear_apply(pia_context* ctx, float* out_br, const float* x_br, const int8_t* w,
+                             const float* scales, int64_t batch, int64_t rows, int64_t cols);
 
 /* KV cache layout (src/memory/layout.rs:17-78): f32
  * [num_layers][num_blocks][block_size][num_kv_heads][k|v][head_dim]. */
@@ -111,6 +114,15 @@ typedef struct pia_attn_entry {
 pia_status pia_paged_attention_dev(pia_context* ctx, float* out, const float* q, const float* kv,
                                    const pia_kv_layout* layout, int64_t num_heads, const pia_attn_entry* entries,
                                    const int32_t* tables, int64_t n, int64_t layer, void* stream);
+
+/* The per-step KV write of run_layers_batch (src/model.rs:1093-1107; single-sequence form
+ * :868-878): k/v [n][num_kv_heads][head_dim] (post-RoPE K, V) stored at each entry's pos, found
+ * through its block table as get_physical_location does; unmapped positions are skipped. Only
+ * pos, table_off and table_len of each entry are read. Block ids are checked against the cache
+ * on the host (the entries and the used table range are read back). */
+pia_status pia_kv_write_dev(pia_context* ctx, float* kv, const pia_kv_layout* layout, const float* k, const float* v,
+                           const pia_attn_entry* entries, const int32_t* tables, int64_t n, int64_t layer,
+                           void* stream);
 
 /* KvLayout::copy_block (src/memory/layout.rs:82-96): copy one physical block, all layers. */
 pia_status pia_kv_copy_block_dev(pia_context* ctx, float* kv, const pia_kv_layout* layout, int64_t src,

@@ -193,6 +193,20 @@ class KvLayout:
         return ((((layer * self.blocks + pb) * self.block_size + off) * self.kv_heads + h) * 2
                 + int(is_value)) * self.head_dim
 
+    def write_token(self, cache, layer, table, pos, k, v):
+        """The per-entry KV write of run_layers_batch (model.rs:1093-1107): k/v [kv_heads][head_dim]
+        stored at pos through the block table (get_physical_location); unmapped -> no write."""
+        loc = table.get_physical_location(pos, self.block_size)
+        if loc is None:
+            return False
+        pb, off = loc
+        for h in range(self.kv_heads):
+            ki = self.index(layer, pb, off, h, False)
+            vi = self.index(layer, pb, off, h, True)
+            cache[ki:ki + self.head_dim] = k[h]
+            cache[vi:vi + self.head_dim] = v[h]
+        return True
+
     def copy_block(self, cache, src: int, dst: int):
         assert src != dst, "copy_block called with src == dst"
         bs = self.block_stride()

@@ -58,6 +58,38 @@ void check_layout(const pia_kv_layout* L) {
               "kv layout dimensions must be positive");
 }
 
+namespace {
+// Reads a launch's device entries and the block-table range they use back to the host and
+// checks them: non-negative fields, and every physical block the kernels will read (logical
+// blocks of start..=pos, or of pos alone when `pos_only`) inside the cache. Out-of-range ids
+// become an error here instead of an out-of-bounds access on the device.
+std::vector<pia_attn_entry> read_checked_entries(const pia_attn_entry* entries, const int32_t* tables, int64_t n,
+                                                 const pia_kv_layout& L, bool pos_only, hipStream_t st) {
+  std::vector<pia_attn_entry> host(n);
+  PIA_HIP(hipMemcpyAsync(host.data(), entries, n * sizeof(pia_attn_entry), hipMemcpyDeviceToHost, st));
+  PIA_HIP(hipStreamSynchronize(st));
+  int64_t need = 0;
+  for (const auto& e : host) {
+    PIA_REQUIRE(e.pos >= 0 && e.start >= 0 && e.table_len >= 0 && e.table_off >= 0, "negative entry field");
+    const int64_t last = std::min<int64_t>(e.table_len, e.pos / L.block_size + 1);
+    if (last > 0) need = std::max<int64_t>(need, e.table_off + last);
+  }
+  if (need == 0) return host;
+  PIA_REQUIRE(tables != nullptr, "null block table");
+  std::vector<int32_t> tab(need);
+  PIA_HIP(hipMemcpyAsync(tab.data(), tables, need * sizeof(int32_t), hipMemcpyDeviceToHost, st));
+  PIA_HIP(hipStreamSynchronize(st));
+  for (const auto& e : host) {
+    const int64_t last = std::min<int64_t>(e.table_len, e.pos / L.block_size + 1);
+    for (int64_t lb = (pos_only ? e.pos : e.start) / L.block_size; lb < last; ++lb) {
+      const int32_t id = tab[e.table_off + lb];
+      PIA_REQUIRE(id >= 0 && id < L.num_blocks, "block table names a block outside the cache");
+    }
+  }
+  return host;
+}
+}  // namespace
+
 // quantize_rows_i8 (src/math.rs:456-469) on the host, rows split over threads (each row is
 // independent, so the split changes no result).
 void quantize_rows_host(const float* w, int64_t rows, int64_t cols, int8_t* q, float* scales) {
@@ -249,10 +281,13 @@ pia_status pia_matvec_i8(pia_context* ctx, float* out, const float* x, const int
   return pia_matmat_i8(ctx, out, x, w, scales, 1, rows, cols);
 }
 
-pia_status pia_matmat_i8(pia_context* ctx, float* out_rb, const float* x_br, const int8_t* w, const float* scales,
-                         int64_t batch, int64_t rows, int64_t cols) {
+namespace {
+// Host-pointer projection: stage w, scales and x on the device, run the int8 GEMV with the
+// given output strides (batch stride osb, row stride osr), copy the result back, synchronize.
+pia_status host_projection(pia_context* ctx, float* out, const float* x_br, const int8_t* w, const float* scales,
+                           int64_t batch, int64_t rows, int64_t cols, int64_t osb, int64_t osr) {
   PIA_API_BEGIN
-  PIA_REQUIRE(ctx && out_rb && x_br && w && scales, "null argument");
+  PIA_REQUIRE(ctx && out && x_br && w && scales, "null argument");
   PIA_REQUIRE(rows > 0 && cols > 0 && batch > 0, "empty shape");
   PIA_HIP(hipSetDevice(ctx->device));
   DeviceBuffer dw, ds, dx, dout;
@@ -265,11 +300,22 @@ pia_status pia_matmat_i8(pia_context* ctx, float* out_rb, const float* x_br, con
   PIA_HIP(hipMemcpyAsync(ds.ptr, scales, rows * sizeof(float), hipMemcpyHostToDevice, st));
   PIA_HIP(hipMemcpyAsync(dx.ptr, x_br, batch * cols * sizeof(float), hipMemcpyHostToDevice, st));
   launch_gemv(GemvArgs{1, dw.ptr, cols, static_cast<const float*>(ds.ptr), static_cast<const float*>(dx.ptr), cols,
-                       nullptr, 0.f, static_cast<float*>(dout.ptr), 1, batch, rows, cols, batch, Epi::Store},
+                       nullptr, 0.f, static_cast<float*>(dout.ptr), osb, osr, rows, cols, batch, Epi::Store},
               st);
-  PIA_HIP(hipMemcpyAsync(out_rb, dout.ptr, batch * rows * sizeof(float), hipMemcpyDeviceToHost, st));
+  PIA_HIP(hipMemcpyAsync(out, dout.ptr, batch * rows * sizeof(float), hipMemcpyDeviceToHost, st));
   PIA_HIP(hipStreamSynchronize(st));
   PIA_API_END
+}
+}  // namespace
+
+pia_status pia_matmat_i8(pia_context* ctx, float* out_rb, const float* x_br, const int8_t* w, const float* scales,
+                         int64_t batch, int64_t rows, int64_t cols) {
+  return host_projection(ctx, out_rb, x_br, w, scales, batch, rows, cols, 1, batch);
+}
+
+pia_status pia_qlinear_apply(pia_context* ctx, float* out_br, const float* x_br, const int8_t* w,
+                             const float* scales, int64_t batch, int64_t rows, int64_t cols) {
+  return host_projection(ctx, out_br, x_br, w, scales, batch, rows, cols, rows, 1);
 }
 
 pia_status pia_paged_attention_dev(pia_context* ctx, float* out, const float* q, const float* kv,
@@ -281,18 +327,12 @@ pia_status pia_paged_attention_dev(pia_context* ctx, float* out, const float* q,
   PIA_REQUIRE(n >= 0, "negative entry count");
   if (n == 0) return PIA_OK;
   PIA_REQUIRE(out && q && kv && entries, "null argument");
-  // Entries live on the device; the split count must cover the widest window, which the host
-  // bounds by the cache capacity (every window is at most num_blocks * block_size ... plus
-  // unmapped tail positions up to the entry's pos). Read the entries back once to size it.
-  std::vector<pia_attn_entry> host(n);
+  // Entries live on the device; the split count must cover the widest window. Read them (and
+  // the block ids they use) back once, to size the split and validate the ids.
   hipStream_t st = stream_of(ctx, stream);
-  PIA_HIP(hipMemcpyAsync(host.data(), entries, n * sizeof(pia_attn_entry), hipMemcpyDeviceToHost, st));
-  PIA_HIP(hipStreamSynchronize(st));
+  const std::vector<pia_attn_entry> host = read_checked_entries(entries, tables, n, *layout, false, st);
   int64_t widest = 1;
-  for (const auto& e : host) {
-    PIA_REQUIRE(e.pos >= 0 && e.start >= 0 && e.table_len >= 0 && e.table_off >= 0, "attention: negative entry field");
-    widest = std::max<int64_t>(widest, e.pos + 1 - e.start);
-  }
+  for (const auto& e : host) widest = std::max<int64_t>(widest, e.pos + 1 - e.start);
   const int64_t hd = layout->head_dim;
   const AttnPlan plan = plan_attention(n, layout->num_kv_heads, hd, widest, ctx->num_cus);
   DeviceBuffer work;
@@ -302,6 +342,22 @@ pia_status pia_paged_attention_dev(pia_context* ctx, float* out, const float* q,
                n, layer, plan, work.ptr, false, nullptr, nullptr};
   launch_attention(a, st);
   PIA_HIP(hipStreamSynchronize(st));
+  PIA_API_END
+}
+
+pia_status pia_kv_write_dev(pia_context* ctx, float* kv, const pia_kv_layout* layout, const float* k, const float* v,
+                           const pia_attn_entry* entries, const int32_t* tables, int64_t n, int64_t layer,
+                           void* stream) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(ctx, "null context");
+  check_layout(layout);
+  PIA_REQUIRE(n >= 0, "negative entry count");
+  PIA_REQUIRE(layer >= 0 && layer < layout->num_layers, "kv_write: layer out of range");
+  if (n == 0) return PIA_OK;
+  PIA_REQUIRE(kv && k && v && entries, "null argument");
+  hipStream_t st = stream_of(ctx, stream);
+  (void)read_checked_entries(entries, tables, n, *layout, true, st);
+  launch_kv_write(k, v, entries, tables, kv, *layout, n, layer, st);
   PIA_API_END
 }
 

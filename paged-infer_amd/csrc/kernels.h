@@ -81,6 +81,11 @@ void launch_rope_kv_write(float* qkv, int64_t ldq, const pia_attn_entry* entries
                           const float* rope_cos, const float* rope_sin, float* kv, const pia_kv_layout& layout,
                           int64_t heads, int64_t batch, int64_t layer, hipStream_t st);
 
+// K/V scatter alone (src/model.rs:1093-1107): k/v rows [n][num_kv_heads * head_dim] to each
+// entry's slot at its pos; entries whose pos is unmapped write nothing.
+void launch_kv_write(const float* k, const float* v, const pia_attn_entry* entries, const int32_t* tables, float* kv,
+                     const pia_kv_layout& layout, int64_t n, int64_t layer, hipStream_t st);
+
 // PagedAttention::run for one layer (see attention.hip). `plan` picks the token split;
 // `work` (attention_work_bytes) is needed when plan.splits > 1 (a combine kernel follows).
 // When `fused`, q rows are the raw qkv rows (RoPE applied in the kernel) and each entry's own

@@ -115,6 +115,27 @@ __global__ __launch_bounds__(kThreads) void k_rope_kv(float* __restrict__ qkv, i
     }
 }
 
+// K/V scatter of one entry per workgroup: k/v rows [n][hkv * hd] to the entry's cache slot
+// (src/model.rs:1093-1107); an unmapped position writes nothing.
+__global__ __launch_bounds__(kThreads) void k_kv_write(const float* __restrict__ k, const float* __restrict__ v,
+                                                       const pia_attn_entry* __restrict__ entries,
+                                                       const int32_t* __restrict__ tables, float* __restrict__ kv,
+                                                       int64_t layer_slots, int block_size, int hkv, int hd) {
+  const int b = blockIdx.x;
+  const pia_attn_entry en = entries[b];
+  const int lb = en.pos / block_size;
+  if (lb >= en.table_len) return;
+  const int64_t slot = static_cast<int64_t>(tables[en.table_off + lb]) * block_size + en.pos % block_size;
+  float* dst = kv + (layer_slots + slot) * hkv * 2 * hd;
+  const float* kr = k + static_cast<int64_t>(b) * hkv * hd;
+  const float* vr = v + static_cast<int64_t>(b) * hkv * hd;
+  for (int idx = threadIdx.x; idx < hkv * hd; idx += kThreads) {
+    const int h = idx / hd, d = idx % hd;
+    dst[static_cast<int64_t>(h) * 2 * hd + d] = kr[idx];
+    dst[(static_cast<int64_t>(h) * 2 + 1) * hd + d] = vr[idx];
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void k_swiglu(const float* __restrict__ gu, int64_t ldgu, float* __restrict__ h,
                                                      int64_t ldh, int inter) {
   const int b = blockIdx.y;
@@ -243,6 +264,17 @@ void launch_rope_kv_write(float* qkv, int64_t ldq, const pia_attn_entry* entries
   hipLaunchKernelGGL(k_rope_kv, dim3(static_cast<unsigned>(batch)), dim3(kThreads), 0, st, qkv, ldq, entries, tables,
                      rope_cos, rope_sin, kv, layer * L.num_blocks * L.block_size, static_cast<int>(L.block_size),
                      static_cast<int>(heads), static_cast<int>(L.num_kv_heads), static_cast<int>(L.head_dim));
+  PIA_HIP(hipGetLastError());
+}
+
+void launch_kv_write(const float* k, const float* v, const pia_attn_entry* entries, const int32_t* tables, float* kv,
+                     const pia_kv_layout& L, int64_t n, int64_t layer, hipStream_t st) {
+  if (n == 0) return;
+  PIA_REQUIRE(layer >= 0 && layer < L.num_layers, "kv_write: layer out of range");
+  PIA_REQUIRE(n < (int64_t(1) << 31), "kv_write: too many entries");
+  hipLaunchKernelGGL(k_kv_write, dim3(static_cast<unsigned>(n)), dim3(kThreads), 0, st, k, v, entries, tables, kv,
+                     layer * L.num_blocks * L.block_size, static_cast<int>(L.block_size),
+                     static_cast<int>(L.num_kv_heads), static_cast<int>(L.head_dim));
   PIA_HIP(hipGetLastError());
 }
 

@@ -47,6 +47,14 @@ def test_int8_projection_matches_oracle(ctx, rows, cols, batch):
     got_rb = out_rb.numpy()
     assert np.all(np.abs(got_rb - ref) <= bound)
     assert np.array_equal(out_br.numpy(), got_rb.T)
+    # Host-pointer forms run the same kernels: identical bits.
+    host_rb = np.empty((rows, batch), np.float32)
+    pia.check(pia.lib().pia_matmat_i8(ctx.h, pia.ptr(host_rb), pia.ptr(x), pia.ptr(q), pia.ptr(s), batch, rows, cols))
+    assert np.array_equal(host_rb, got_rb)
+    host_br = np.empty((batch, rows), np.float32)
+    pia.check(pia.lib().pia_qlinear_apply(ctx.h, pia.ptr(host_br), pia.ptr(x), pia.ptr(q), pia.ptr(s), batch, rows,
+                                          cols))
+    assert np.array_equal(host_br, got_rb.T)
     if batch == 1:
         out = np.empty(rows, np.float32)
         pia.check(pia.lib().pia_matvec_i8(ctx.h, pia.ptr(out), pia.ptr(x[0]), pia.ptr(q), pia.ptr(s), rows, cols))
@@ -109,6 +117,41 @@ def test_paged_attention_matches_oracle(ctx, case):
                                                 len(entries), 1, None))
     got = out.numpy()
     assert np.allclose(got, ref, atol=1e-5, rtol=1e-5), np.max(np.abs(got - ref))
+
+
+def test_kv_write_matches_oracle(ctx):
+    # The standalone KV scatter (model.rs:1093-1107): mapped positions land where the layout
+    # says, unmapped ones (entry 2) write nothing, other layers are untouched.
+    layout = (3, 9, 4, 2, 8)
+    rng = np.random.default_rng(11)
+    L, oL = pia.KvLayout(*layout), om.KvLayout(*layout)
+    kv = rng.normal(size=oL.total_floats()).astype(np.float32)
+    tables = [[7, 2, 5], [0], [3]]
+    entries = [(9, 0), (3, 0), (4, 0)]  # entry 2: logical block 1 is past its table
+    n, hkv, hd = len(entries), layout[3], layout[4]
+    k = rng.normal(size=(n, hkv, hd)).astype(np.float32)
+    v = rng.normal(size=(n, hkv, hd)).astype(np.float32)
+    ref = kv.copy()
+    for i, (pos, _) in enumerate(entries):
+        t = om.BlockTable()
+        for b in tables[i]:
+            t.append_block(b)
+        oL.write_token(ref, 1, t, pos, k[i], v[i])
+    ent, flat = _attn_entries(entries, tables)
+    dkv, dk, dv, de, dt = ctx.to_device(kv), ctx.to_device(k), ctx.to_device(v), ctx.to_device(ent), ctx.to_device(flat)
+    print("[kv_write] layout", layout, flush=True)
+    pia.check(pia.lib().pia_kv_write_dev(ctx.h, dkv.ptr, L, dk.ptr, dv.ptr, de.ptr, dt.ptr, n, 1, None))
+    ctx.sync()
+    assert np.array_equal(dkv.numpy(), ref)
+    # Out-of-range block ids and layers are rejected on the host before any launch.
+    bad = ctx.to_device(np.array([7, 2, 99, 0, 3], np.int32))
+    assert pia.lib().pia_kv_write_dev(ctx.h, dkv.ptr, L, dk.ptr, dv.ptr, de.ptr, bad.ptr, n, 1, None) != 0
+    assert pia.lib().pia_kv_write_dev(ctx.h, dkv.ptr, L, dk.ptr, dv.ptr, de.ptr, dt.ptr, n, 3, None) != 0
+    out = ctx.empty((n, 4 * hd), np.float32)
+    q = ctx.to_device(rng.normal(size=(n, 4 * hd)).astype(np.float32))
+    assert pia.lib().pia_paged_attention_dev(ctx.h, out.ptr, q.ptr, dkv.ptr, L, 4, de.ptr, bad.ptr, n, 1, None) != 0
+    ctx.sync()
+    assert np.array_equal(dkv.numpy(), ref)
 
 
 def test_copy_block_and_device_cow(ctx):

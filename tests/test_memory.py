@@ -312,3 +312,22 @@ def test_differential_random_operations():
                 assert py.blocks(tables_py[s]) == cc.blocks(tables_cc[s])
             for blk in range(total):
                 assert py.ref_count(blk) == cc.ref_count(blk)
+
+
+def test_kv_layout_write_matches_dimension_order():
+    # layout.rs:17-78 fixes [layer][block][token][kv_head][k|v][head_dim]; a 6-D view of the
+    # flat cache in that order must see exactly what write_token stored.
+    dims = (3, 5, 4, 2, 6)
+    L = om.KvLayout(*dims)
+    cache = np.zeros(L.total_floats(), np.float32)
+    view = cache.reshape(dims[0], dims[1], dims[2], dims[3], 2, dims[4])
+    t = om.BlockTable()
+    for b in (4, 1):
+        t.append_block(b)
+    rng = np.random.default_rng(0)
+    k, v = rng.normal(size=(2, 6)).astype(np.float32), rng.normal(size=(2, 6)).astype(np.float32)
+    assert L.write_token(cache, 2, t, 6, k, v)  # logical block 1 -> block 1, offset 2
+    assert np.array_equal(view[2, 1, 2, :, 0], k) and np.array_equal(view[2, 1, 2, :, 1], v)
+    assert np.count_nonzero(cache) == k.size + v.size
+    assert not L.write_token(cache, 0, t, 8, k, v)  # logical block 2 unmapped: nothing written
+    assert np.count_nonzero(cache) == k.size + v.size
