@@ -278,7 +278,9 @@ struct pia_model {
 
   // run_layers_batch (src/model.rs:968-1177) for `n` rows whose step inputs are already on the
   // device; leaves the residual stream (before the final norm) in x.
-  void run_layers(int64_t n, const StepDev& in, const AttnPlan& plan, bool fused, int64_t mapped_tokens) {
+  // `prefill`: the entries are consecutive positions of one sequence sharing one table.
+  void run_layers(int64_t n, const StepDev& in, const AttnPlan& plan, bool fused, int64_t mapped_tokens,
+                  bool prefill = false) {
     const auto& c = cfg;
     const int64_t attn_bytes = mapped_tokens * c.kv_heads * 2 * hd * 4 + 2 * n * c.hidden * 4;
     float* X = x.as<float>();
@@ -296,7 +298,7 @@ struct pia_model {
           launch_rope_kv_write(QKV, ld_qkv, in.entries, in.tables, rope_cos.as<float>(), rope_sin.as<float>(),
                                kv.as<float>(), layout, c.heads, n, l, st());
         AttnLaunch a{QKV, ld_qkv, ATT, ld_h, kv.as<float>(), &layout, c.heads, in.entries, in.tables, n, l, plan,
-                     attn_work.ptr, fused, rope_cos.as<float>(), rope_sin.as<float>()};
+                     attn_work.ptr, fused, rope_cos.as<float>(), rope_sin.as<float>(), prefill};
         launch_attention(a, st());
       });
       gemv(L.o, ATT, ld_h, nullptr, X, ld_h, n, Epi::Add);
@@ -965,7 +967,7 @@ pia_status pia_model_prefill(pia_model* m, const uint32_t* tokens, int64_t n, in
   if (wb) m->grow(m->attn_work, wb);
   const pia_model::StepDev in = upload_step(m, tok, ent, table, table_len);
   m->run_step({1, n, plan.split, plan.splits, plan.chunk, fused ? 1 : 0}, false, [&] {
-    m->run_layers(n, in, plan, fused, mapped);
+    m->run_layers(n, in, plan, fused, mapped, true);
     // Only the last position pays for the LM head (src/model.rs:1249-1254).
     m->normed_gemv(m->lm_head, m->x.as<float>() + (n - 1) * m->ld_h, m->final_norm.as<float>(), 1,
                    m->logits.as<float>(), m->ld_v, Epi::Store, m->amax.as<unsigned long long>());

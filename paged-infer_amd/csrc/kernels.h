@@ -114,7 +114,12 @@ struct AttnLaunch {
   bool fused;
   const float* rope_cos;
   const float* rope_sin;
+  // Entries are consecutive positions of one sequence sharing one block table (a prefill):
+  // from kPrefillTileMin entries (head_dim 64 or 128, not fused) a query-tiled kernel runs
+  // instead, which reads each K/V row once per tile of positions.
+  bool prefill = false;
 };
+constexpr int64_t kPrefillTileMin = 64;
 void launch_attention(const AttnLaunch& a, hipStream_t st);
 
 // Spin for about `us` microseconds (one thread; bounded by the device clock). Used only to let

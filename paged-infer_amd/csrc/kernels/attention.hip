@@ -343,6 +343,302 @@ __global__ __launch_bounds__(kMaxHd) void k_attn_combine(const float* __restrict
   out[static_cast<int64_t>(e) * ldo + h * hd + t] = lsum > 0.0f ? acc / lsum : 0.0f;
 }
 
+// ---------------------------------------------------------------------------------------
+// Prefill attention: the entries of one launch are consecutive positions of one sequence
+// sharing one block table (prefill_batched, src/model.rs:1222-1255), and their K/V are
+// already in the cache. A workgroup owns R query rows of one kv head (QT = R / G
+// consecutive positions times the G heads of the group, row r = query (r / G), head
+// kvh * G + r % G) and walks the tokens its positions attend to in chunks of kPfChunk,
+// staged in LDS, so each K and V row is read once per R rows instead of once per G.
+// Scores, online softmax and P.V run on register tiles: thread (rg, tg) owns rows
+// rg * RPT .. + RPT and, per chunk, the tokens tg + 16 j (scores) or the dims tg * 4 + 64 w
+// (output). The next chunk's block ids are resolved during the scores and its K/V loads
+// are in flight during P.V.
+constexpr int kPfPad = 4;  // floats of padding per LDS row of Q, K and P (bank spread)
+
+__device__ inline void fma4(float* o, float p, const float4& v) {
+  o[0] = __builtin_fmaf(p, v.x, o[0]);
+  o[1] = __builtin_fmaf(p, v.y, o[1]);
+  o[2] = __builtin_fmaf(p, v.z, o[2]);
+  o[3] = __builtin_fmaf(p, v.w, o[3]);
+}
+
+// Query-head rows per workgroup. Taller tiles reuse each K/V row more but their LDS and
+// registers leave fewer waves per CU to hide LDS latency: 32 measured best of 16/32/64/128 on
+// 2048-token TinyLlama prefills.
+template <int HD>
+constexpr int pf_rows() {
+  return 32;
+}
+// Tokens per chunk: 64, or 32 at head_dim 128 (keeps the LDS of a workgroup near 55 KB so
+// that two or three fit on a CU).
+template <int HD>
+constexpr int pf_chunk() {
+  return HD <= 64 ? 64 : 32;
+}
+
+struct PfParams {
+  const float* q;  // rows [n][ldq]: head h at column h * hd (post-RoPE)
+  int64_t ldq;
+  float* out;
+  int64_t ldo;
+  const float* kv;
+  int64_t layer_slots;
+  int block_size, hkv, heads, n;
+  float scale;
+  const pia_attn_entry* entries;
+  const int32_t* tables;
+};
+
+template <int G, int HD>
+__global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
+  constexpr int R = pf_rows<HD>();
+  constexpr int kPfChunk = pf_chunk<HD>();
+  constexpr int TJ = kPfChunk / 16;  // tokens per thread in the scores
+  constexpr int QT = R / G;         // query positions per workgroup
+  constexpr int RPT = R / 16;       // rows per thread
+  constexpr int QS = HD + kPfPad;   // LDS row stride of Q and K
+  constexpr int PS = kPfChunk + kPfPad;
+  constexpr int W = HD / 64;        // float4 dim groups per thread in P.V (dims tg*4 + 64 w)
+  constexpr int KV4 = kPfChunk * HD / 4 / kThreads;  // float4 of K (and of V) per thread per chunk
+  static_assert(HD % 64 == 0 && R % 16 == 0 && QT >= 1 && KV4 >= 1, "prefill attention tile shape");
+  extern __shared__ __align__(16) float smem[];
+  float* Qs = smem;                  // [R][QS]
+  float* Ks = Qs + R * QS;           // [kPfChunk][QS]
+  float* Vs = Ks + kPfChunk * QS;    // [kPfChunk][HD]
+  float* Ps = Vs + kPfChunk * HD;    // [R][PS]
+  int* slots = reinterpret_cast<int*>(Ps + R * PS);  // [2][kPfChunk]
+  int* qpos = slots + 2 * kPfChunk;  // [QT]
+  int* qstart = qpos + QT;           // [QT]
+
+  const int tid = threadIdx.x;
+  const int kvh = blockIdx.y;
+  // The longest windows (last positions) first: they take the most chunks.
+  const int tile = gridDim.x - 1 - blockIdx.x;
+  const int e0 = tile * QT;
+  const pia_attn_entry first = p.entries[e0];
+  const int table_off = first.table_off, table_len = first.table_len;
+  for (int i = tid; i < QT; i += kThreads) {
+    const int e = e0 + i;
+    if (e < p.n) {
+      const pia_attn_entry en = p.entries[e];
+      qpos[i] = en.pos;
+      qstart[i] = en.start;
+    } else {
+      qpos[i] = -1;  // no such query: every token masked, nothing written
+      qstart[i] = 0x7fffffff;
+    }
+  }
+  for (int i = tid; i < R * (HD / 4); i += kThreads) {
+    const int r = i / (HD / 4), d = (i % (HD / 4)) * 4;
+    const int e = e0 + r / G;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (e < p.n)
+      v = *reinterpret_cast<const float4*>(p.q + static_cast<int64_t>(e) * p.ldq + (kvh * G + r % G) * HD + d);
+    *reinterpret_cast<float4*>(Qs + r * QS + d) = v;
+  }
+  __syncthreads();
+  int lo = 0x7fffffff, hi = -1;
+  for (int i = 0; i < QT; ++i)
+    if (qpos[i] >= 0) lo = min(lo, qstart[i]), hi = max(hi, qpos[i]);
+  if (hi < 0) return;  // uniform over the workgroup
+  const int nchunks = hi >= lo ? (hi - lo) / kPfChunk + 1 : 0;
+
+  auto resolve = [&](int c, int* dst) {  // block ids of chunk c (threads < kPfChunk)
+    if (tid < kPfChunk) {
+      const int t = lo + c * kPfChunk + tid;
+      int slot = -1;
+      if (t <= hi) {
+        const int lb = t / p.block_size;
+        if (lb < table_len) slot = p.tables[table_off + lb] * p.block_size + t % p.block_size;
+      }
+      dst[tid] = slot;
+    }
+  };
+  const int64_t head_stride = 2 * static_cast<int64_t>(HD);
+  float4 kreg[KV4], vreg[KV4];
+  auto load = [&](const int* sl) {
+#pragma unroll
+    for (int u = 0; u < KV4; ++u) {
+      const int i = tid + u * kThreads;
+      const int t = i / (HD / 4), d = (i % (HD / 4)) * 4;
+      // Unmapped tokens read slot 0 of the layer (always inside the cache) and are zeroed.
+      const int slot = sl[t];
+      const float* src = p.kv + ((p.layer_slots + max(slot, 0)) * p.hkv + kvh) * head_stride + d;
+      const float4 k4 = *reinterpret_cast<const float4*>(src);
+      const float4 v4 = *reinterpret_cast<const float4*>(src + HD);
+      const bool keep = slot >= 0;
+      kreg[u] = make_float4(keep ? k4.x : 0.f, keep ? k4.y : 0.f, keep ? k4.z : 0.f, keep ? k4.w : 0.f);
+      vreg[u] = make_float4(keep ? v4.x : 0.f, keep ? v4.y : 0.f, keep ? v4.z : 0.f, keep ? v4.w : 0.f);
+    }
+  };
+
+  const int rg = tid / 16, tg = tid % 16;
+  float m[RPT], l[RPT], o[RPT][W][4];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) o[i][w][0] = o[i][w][1] = o[i][w][2] = o[i][w][3] = 0.0f;
+  }
+
+  if (nchunks > 0) {
+    resolve(0, slots);
+    __syncthreads();
+    load(slots);
+  }
+  for (int c = 0; c < nchunks; ++c) {
+    const int* cur = slots + (c & 1) * kPfChunk;
+    int* nxt = slots + ((c + 1) & 1) * kPfChunk;
+    const int c0 = lo + c * kPfChunk;
+#pragma unroll
+    for (int u = 0; u < KV4; ++u) {
+      const int i = tid + u * kThreads;
+      const int t = i / (HD / 4), d = (i % (HD / 4)) * 4;
+      *reinterpret_cast<float4*>(Ks + t * QS + d) = kreg[u];
+      *reinterpret_cast<float4*>(Vs + t * HD + d) = vreg[u];
+    }
+    __syncthreads();
+    if (c + 1 < nchunks) resolve(c + 1, nxt);
+
+    // Scores of rows rg*RPT+i against tokens tg + 16 j.
+    float s[RPT][TJ];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) s[i][j] = 0.0f;
+#pragma unroll 4
+    for (int d = 0; d < HD; d += 4) {
+      float4 k4[TJ];
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) k4[j] = *reinterpret_cast<const float4*>(Ks + (tg + 16 * j) * QS + d);
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) {
+        const float4 q4 = *reinterpret_cast<const float4*>(Qs + (rg * RPT + i) * QS + d);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          s[i][j] = __builtin_fmaf(q4.x, k4[j].x, s[i][j]);
+          s[i][j] = __builtin_fmaf(q4.y, k4[j].y, s[i][j]);
+          s[i][j] = __builtin_fmaf(q4.z, k4[j].z, s[i][j]);
+          s[i][j] = __builtin_fmaf(q4.w, k4[j].w, s[i][j]);
+        }
+      }
+    }
+    float alpha[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int r = rg * RPT + i;
+      const int pos = qpos[r / G], st = qstart[r / G];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const int tk = tg + 16 * j;
+        const int t = c0 + tk;
+        const bool ok = cur[tk] >= 0 && t >= st && t <= pos;
+        s[i][j] = ok ? s[i][j] * p.scale : -INFINITY;
+        mx = fmaxf(mx, s[i][j]);
+      }
+#pragma unroll
+      for (int off = 8; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      const float m_new = fmaxf(m[i], mx);
+      float sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const float pr = (m_new == -INFINITY) ? 0.0f : expf(s[i][j] - m_new);
+        Ps[r * PS + tg + 16 * j] = pr;
+        sum += pr;
+      }
+#pragma unroll
+      for (int off = 8; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+      alpha[i] = (m[i] == -INFINITY) ? 0.0f : expf(m[i] - m_new);
+      l[i] = __builtin_fmaf(l[i], alpha[i], sum);
+      m[i] = m_new;
+    }
+    __syncthreads();  // P complete; the next chunk's block ids resolved
+    if (c + 1 < nchunks) load(nxt);
+
+    // O[r][d] = O * alpha + sum_t P[r][t] V[t][d], dims tg*4 + 64 w.
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+#pragma unroll
+      for (int w = 0; w < W; ++w)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[i][w][k] *= alpha[i];
+#pragma unroll 2
+    for (int t = 0; t < kPfChunk; t += 4) {
+      float4 v4[4][W];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int w = 0; w < W; ++w) v4[u][w] = *reinterpret_cast<const float4*>(Vs + (t + u) * HD + tg * 4 + 64 * w);
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) {
+        const float4 p4 = *reinterpret_cast<const float4*>(Ps + (rg * RPT + i) * PS + t);
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          fma4(o[i][w], p4.x, v4[0][w]);
+          fma4(o[i][w], p4.y, v4[1][w]);
+          fma4(o[i][w], p4.z, v4[2][w]);
+          fma4(o[i][w], p4.w, v4[3][w]);
+        }
+      }
+    }
+    __syncthreads();  // Ks / Vs / Ps are rewritten by the next chunk
+  }
+
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int r = rg * RPT + i;
+    const int e = e0 + r / G;
+    if (e >= p.n) continue;
+    float* dst = p.out + static_cast<int64_t>(e) * p.ldo + (kvh * G + r % G) * HD;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      float4 v;
+      v.x = l[i] > 0.0f ? o[i][w][0] / l[i] : 0.0f;
+      v.y = l[i] > 0.0f ? o[i][w][1] / l[i] : 0.0f;
+      v.z = l[i] > 0.0f ? o[i][w][2] / l[i] : 0.0f;
+      v.w = l[i] > 0.0f ? o[i][w][3] / l[i] : 0.0f;
+      *reinterpret_cast<float4*>(dst + tg * 4 + 64 * w) = v;
+    }
+  }
+}
+
+template <int HD>
+size_t pf_smem_bytes() {
+  constexpr int R = pf_rows<HD>();
+  constexpr int kPfChunk = pf_chunk<HD>();
+  return sizeof(float) * (R * (HD + kPfPad) + kPfChunk * (HD + kPfPad) + kPfChunk * HD + R * (kPfChunk + kPfPad)) +
+         sizeof(int) * (2 * kPfChunk + 2 * R);
+}
+
+template <int G, int HD>
+void go_prefill(const PfParams& p, hipStream_t st) {
+  constexpr int QT = pf_rows<HD>() / G;
+  const size_t smem = pf_smem_bytes<HD>();
+  static bool done = false;
+  if (!done) {
+    PIA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_prefill<G, HD>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
+    done = true;
+  }
+  dim3 grid(static_cast<unsigned>((p.n + QT - 1) / QT), static_cast<unsigned>(p.hkv));
+  hipLaunchKernelGGL((k_attn_prefill<G, HD>), grid, dim3(kThreads), smem, st, p);
+}
+
+template <int HD>
+void prefill_by_g(const PfParams& p, int g, hipStream_t st) {
+  switch (g) {
+    case 1: go_prefill<1, HD>(p, st); break;
+    case 2: go_prefill<2, HD>(p, st); break;
+    case 4: go_prefill<4, HD>(p, st); break;
+    case 8: go_prefill<8, HD>(p, st); break;
+    case 16: go_prefill<16, HD>(p, st); break;
+    default: fail(PIA_ERR_INVALID, "attention: kv_group must be 1, 2, 4, 8 or 16");
+  }
+}
+
 size_t attn_smem_bytes(int g, int hd, int chunk) {
   const int ngrp = kThreads / (hd / 4);
   return sizeof(float) * (g * hd + g * chunk + 4 * g + 2 * hd) + sizeof(int) * chunk + sizeof(float) * ngrp * g * hd;
@@ -449,6 +745,22 @@ void launch_attention(const AttnLaunch& a, hipStream_t st) {
   if (a.n == 0) return;
   const int g = static_cast<int>(a.heads / L.num_kv_heads);
   const int hd = static_cast<int>(L.head_dim);
+  // PIA_PREFILL_TILE_MIN overrides the entry count from which prefills use the tiled kernel.
+  static const int64_t tile_min = [] {
+    const char* e = std::getenv("PIA_PREFILL_TILE_MIN");
+    const long v = e ? std::strtol(e, nullptr, 10) : 0;
+    return v > 0 ? static_cast<int64_t>(v) : kPrefillTileMin;
+  }();
+  if (a.prefill && !a.fused && a.n >= tile_min && (hd == 64 || hd == 128)) {
+    PIA_REQUIRE(a.n < (int64_t(1) << 31), "attention: too many entries");
+    PfParams pf{a.q,       a.ldq,  a.out, a.ldo, a.kv, a.layer * L.num_blocks * L.block_size, static_cast<int>(L.block_size),
+                static_cast<int>(L.num_kv_heads), static_cast<int>(a.heads), static_cast<int>(a.n),
+                1.0f / sqrtf(static_cast<float>(hd)), a.entries, a.tables};
+    if (hd == 64) prefill_by_g<64>(pf, g, st);
+    else prefill_by_g<128>(pf, g, st);
+    PIA_HIP(hipGetLastError());
+    return;
+  }
   AttnParams p;
   p.q = a.q;
   p.ldq = a.ldq;

@@ -145,6 +145,51 @@ def test_prefill_tiled_gemm_ragged_shapes(ctx):
     assert g == c and rel <= LOGIT_TOL
 
 
+PREFILL_ATTN = [  # hidden, heads, kv_heads, window, prompt tokens, resume split
+    (512, 8, 1, None, 203, 0),    # head_dim 64, 8 heads per kv head, ragged last tile
+    (512, 8, 2, None, 187, 37),   # second prefill starts at position 37 (tile window not chunk-aligned)
+    (256, 4, 4, 45, 130, 0),      # one head per kv head, sliding window of 45
+    (512, 4, 2, None, 100, 0),    # head_dim 128
+    (1024, 8, 4, 70, 160, 64),    # head_dim 128, window, resumed prefill
+]
+
+
+@pytest.mark.parametrize("case", range(len(PREFILL_ATTN)))
+def test_prefill_tiled_attention(ctx, case):
+    """Prefills of 64 or more positions run the query-tiled attention kernel (32 query-head
+    rows per workgroup: 32/G positions x the G heads of a kv head; K/V staged in LDS by 64-token
+    chunks, 32 at head_dim 128). Logits of the last position and the K/V written by the prefill (through
+    the greedy decode steps that follow) are compared with the oracle."""
+    hidden, heads, kvh, window, n, split = PREFILL_ATTN[case]
+    print(f"[prefill-attn] hidden={hidden} heads={heads} kv={kvh} window={window} n={n} split={split}", flush=True)
+    cfg = pia.LlamaConfig(hidden=hidden, layers=2, heads=heads, kv_heads=kvh, inter=344, vocab=512,
+                          attention_window=window)
+    w = pia.synth_weights(cfg, seed=20 + case)
+    prompt = np.random.default_rng(20 + case).integers(0, cfg.vocab, n).tolist()
+    if split == 0:
+        g, c, rel = greedy_session(ctx, cfg, w, prompt, 6)
+        assert g == c and rel <= LOGIT_TOL, (g, c, rel)
+        return
+    bs = 16
+    nb = (n + 8 + bs - 1) // bs
+    table = list(range(nb))
+    gm = pia.Model(ctx, cfg, w)
+    gm.kv_alloc(nb + 1, bs)
+    om_ = orc.OracleModel(cfg, w)
+    kv = np.zeros(orc.kv_floats(cfg, nb + 1, bs), np.float32)
+    gm.prefill(prompt[:split], 0, table)
+    om_.prefill(prompt[:split], 0, table, kv, nb + 1, bs)
+    lg, tg = gm.prefill(prompt[split:], split, table)
+    lc = om_.prefill(prompt[split:], split, table, kv, nb + 1, bs)
+    assert tg == orc.argmax(lc) and _rel(lg, lc) <= LOGIT_TOL
+    for i in range(4):
+        lg, am = gm.decode([tg], [n + i], [table])
+        lc = om_.decode([tg], [n + i], [table], kv, nb + 1, bs)
+        assert int(am[0]) == orc.argmax(lc[0]) and _rel(lg[0], lc[0]) <= LOGIT_TOL
+        tg = int(am[0])
+    gm.close()
+
+
 def test_persistent_step_llama3_shape(ctx):
     """The persistent step at Llama-3-8B layer shapes (hidden 4096, 32/8 heads, head_dim 128,
     FFN 14336, rotary theta 500000), two layers and a 16k vocabulary to keep the oracle fast:
