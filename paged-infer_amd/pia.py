@@ -1,8 +1,10 @@
 """ctypes binding of libpaged_infer_amd.so (the C ABI declared in include/paged_infer_amd.h).
 
 This is the reference-side binding a Python caller uses; it mirrors the reference's seams:
-  - kernel tier:  quantize_rows_i8 / matvec_i8 / matmat_i8 (src/math.rs), PagedAttention::run
-                  (src/attention.rs), KvLayout::copy_block (src/memory/layout.rs)
+  - kernel tier:  quantize_rows_i8 / matvec_i8 / matmat_i8 (src/math.rs), Projection::
+                  apply_batched (src/model.rs:247-259), PagedAttention::run (src/attention.rs),
+                  the per-step KV write (src/model.rs:1093-1107), KvLayout::copy_block
+                  (src/memory/layout.rs)
   - memory tier:  KvCacheManager / BlockTable / block_hash (src/memory/*.rs)
   - model tier:   LlamaWeights::decode_batch_into / prefill_batched (src/model.rs:1184-1255)
 It never falls back to anything: when the library is missing or no gfx950 device is present,
