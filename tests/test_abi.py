@@ -58,3 +58,12 @@ def test_errors_are_status_codes_not_crashes():
     h = ctypes.c_void_p()
     with pytest.raises(pia.PiaError, match="bad pool shape"):
         pia.check(pia.lib().pia_kvm_create(4, 0, 1, ctypes.byref(h)))
+    # Kernel-tier entry points validate before touching the device.
+    with pytest.raises(pia.PiaError, match="null"):
+        pia.check(pia.lib().pia_qlinear_apply(None, None, None, None, None, 1, 1, 1))
+    with pytest.raises(pia.PiaError, match="null context"):
+        pia.check(pia.lib().pia_kv_write_dev(None, None, pia.KvLayout(1, 1, 1, 1, 4), None, None, None, None,
+                                             1, 0, None))
+    with pytest.raises(pia.PiaError, match="null context"):
+        pia.check(pia.lib().pia_paged_attention_dev(None, None, None, None, pia.KvLayout(1, 1, 1, 1, 4), 1, None,
+                                                    None, 1, 0, None))
