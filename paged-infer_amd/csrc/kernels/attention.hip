@@ -355,6 +355,7 @@ __global__ __launch_bounds__(kMaxHd) void k_attn_combine(const float* __restrict
 // (output). The next chunk's block ids are resolved during the scores and its K/V loads
 // are in flight during P.V.
 constexpr int kPfPad = 4;  // floats of padding per LDS row of Q, K and P (bank spread)
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ inline void fma4(float* o, float p, const float4& v) {
   o[0] = __builtin_fmaf(p, v.x, o[0]);
@@ -502,29 +503,50 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
     __syncthreads();
     if (c + 1 < nchunks) resolve(c + 1, nxt);
 
-    // Scores of rows rg*RPT+i against tokens tg + 16 j.
+    // Scores on the f32 matrix cores: wave w computes TPW 16x16 tiles of S = Q K^T (rows
+    // rt*16.., tokens tt*16..), the head dimension split into four contiguous quarters, one
+    // per 16-lane group (any order of the dot product's terms is the same sum, rounded
+    // differently). S goes to Ps, then each thread reads its (row, token) elements.
+    {
+      constexpr int NTT = kPfChunk / 16;           // token tiles per chunk
+      constexpr int TPW = (R / 16) * NTT / 4;      // tiles per wave
+      constexpr int KL = HD / 4;                   // head dims per lane group
+      static_assert(TPW >= 1 && (R / 16) * NTT % 4 == 0 && NTT % TPW == 0, "score tiles per wave");
+      const int wave = tid >> 6, lane = tid & 63, lr = lane & 15, kq = lane >> 4;
+      const int tile0 = wave * TPW, rt = tile0 / NTT;
+      f32x4 acc[TPW];
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const float* qa = Qs + (rt * 16 + lr) * QS + kq * KL;
+#pragma unroll
+      for (int k4 = 0; k4 < KL; k4 += 4) {
+        const float4 a = *reinterpret_cast<const float4*>(qa + k4);
+        float4 b[TPW];
+#pragma unroll
+        for (int j = 0; j < TPW; ++j)
+          b[j] = *reinterpret_cast<const float4*>(Ks + (((tile0 + j) % NTT) * 16 + lr) * QS + kq * KL + k4);
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) {
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b[j].x, acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b[j].y, acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b[j].z, acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b[j].w, acc[j], 0, 0, 0);
+        }
+      }
+      // Result layout: lane holds rows 4 * (lane / 16) + v of the tile, token lane % 16.
+#pragma unroll
+      for (int j = 0; j < TPW; ++j) {
+        const int tt = (tile0 + j) % NTT;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) Ps[(rt * 16 + 4 * kq + v) * PS + tt * 16 + lr] = acc[j][v];
+      }
+    }
+    __syncthreads();
     float s[RPT][TJ];
 #pragma unroll
     for (int i = 0; i < RPT; ++i)
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) s[i][j] = 0.0f;
-#pragma unroll 4
-    for (int d = 0; d < HD; d += 4) {
-      float4 k4[TJ];
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) k4[j] = *reinterpret_cast<const float4*>(Ks + (tg + 16 * j) * QS + d);
-#pragma unroll
-      for (int i = 0; i < RPT; ++i) {
-        const float4 q4 = *reinterpret_cast<const float4*>(Qs + (rg * RPT + i) * QS + d);
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-          s[i][j] = __builtin_fmaf(q4.x, k4[j].x, s[i][j]);
-          s[i][j] = __builtin_fmaf(q4.y, k4[j].y, s[i][j]);
-          s[i][j] = __builtin_fmaf(q4.z, k4[j].z, s[i][j]);
-          s[i][j] = __builtin_fmaf(q4.w, k4[j].w, s[i][j]);
-        }
-      }
-    }
+      for (int j = 0; j < TJ; ++j) s[i][j] = Ps[(rg * RPT + i) * PS + tg + 16 * j];
     float alpha[RPT];
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
