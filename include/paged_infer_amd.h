@@ -81,7 +81,11 @@ pia_status pia_matvec_i8_dev(pia_context* ctx, float* out, const float* x, const
                              int64_t rows, int64_t cols, void* stream);
 
 /* matmat_i8_weight_parallel (src/math.rs:223-275): out_rb[r][b] = dot(W[r], x_br[b]) * s[r].
- * Output is [row][batch], as in the reference (the caller transposes). */
+ * Output is [row][batch], as in the reference (the caller transposes). From 5 batch rows, when
+ * cols is a multiple of 64 and the pointers are 16-byte aligned, the matmat and apply forms run on
+ * the int8 matrix cores (activations as three 8-bit digits of a 23-bit fixed-point image per row,
+ * exact integer accumulation; |error| <= 2^-23 * 2^e * sum|w| * scale per output, max|x_b| < 2^e)
+ * with the digits in the context's workspace: calls on one context must not overlap. */
 pia_status pia_matmat_i8(pia_context* ctx, float* out_rb, const float* x_br, const int8_t* w, const float* scales,
                          int64_t batch, int64_t rows, int64_t cols);
 pia_status pia_matmat_i8_dev(pia_context* ctx, float* out_rb, const float* x_br, const int8_t* w,
@@ -357,7 +361,8 @@ pia_status pia_model_bench_class(pia_model* m, int32_t cls, int64_t batch, int32
  * replay; *us = mean microseconds per launch. Also reports the launch's
  * algorithmic bytes (int8 weights + scales + activations in + results out). */
 /* flags: 1 = fused RMSNorm prologue, 2 = SwiGLU epilogue, 4 = residual-add epilogue,
- * 8 = matrix-core path (digit split; the digit conversion is timed with it). */
+ * 8 = matrix-core path (digit split; the digit conversion is timed with it), 16 (with 8) = the
+ * digits are written once before the timed launches, which then time the projection alone. */
 pia_status pia_bench_projection(pia_context* ctx, int64_t rows, int64_t cols, int64_t batch, int32_t reps,
                                 int32_t flags, double* us, int64_t* bytes);
 

@@ -7,6 +7,7 @@
 #include <cstdint>
 
 #include "paged_infer_amd.h"
+#include "../kernels.h"
 
 namespace pia {
 
@@ -53,6 +54,8 @@ struct pia_context {
   int num_cus = 0;
   hipStream_t stream = nullptr;
   pia::DeviceBuffer sample_ws;  // sort keys / indices / probabilities of pia_sample_dev
+  // Kernel-tier projections on the matrix cores: activation digits, split-K partials + counters.
+  pia::DeviceBuffer proj_digits, proj_split;
 };
 
 namespace pia {
@@ -64,6 +67,10 @@ void quantize_rows_host(const float* w, int64_t rows, int64_t cols, int8_t* q, f
 // pia_sample_dev with the context's workspace, on stream st.
 void sample_with_context(pia_context* ctx, int32_t* out, const float* logits, int64_t ld, int64_t n, int64_t vocab,
                          const pia_sampling* params, uint64_t* rng_state, int32_t mode, hipStream_t st);
+// The kernel tier's int8 projection (matvec / matmat / apply_batched): batches of at least
+// kMfmaMinBatch rows whose rows are whole 64-byte k-steps run the matrix-core path (digits in
+// the context's workspace, so calls on one context must be ordered), the rest the GEMV.
+void launch_projection(pia_context* ctx, const GemvArgs& g, hipStream_t st);
 void model_set_proj_bf16_dev(pia_model* m, int64_t layer, int32_t which, int kind, const uint16_t* src, int64_t rows,
                              int64_t cols);
 }  // namespace pia

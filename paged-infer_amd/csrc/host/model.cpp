@@ -25,8 +25,6 @@ inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
 // Rows up to which RMSNorm is fused into the projection that consumes it.
 constexpr int64_t kFusedNormRows = 64;
-// Batch from which int8 projections run on the matrix cores instead of the streaming GEMV.
-constexpr int64_t kMfmaMinBatch = 5;
 // 16-row tiles the decode GEMM's split-K workspace covers (255 tiles x 8 slices x 8 KiB).
 constexpr int64_t kDecSplitTiles = 255;
 
@@ -101,6 +99,7 @@ struct pia_model {
   DeviceBuffer dec_split;  // split-K partial sums and counters of the decode GEMM
   bool dec_split_on = true;
   int64_t mfma_min = kMfmaMinBatch;
+  bool replay_graphs = true;  // diagnostic PIA_NO_GRAPH=1: decode steps launch eagerly
   int64_t logit_rows = 0;  // rows of `logits` the last decode / prefill wrote
   DeviceBuffer samp;       // sampling parameters, generator states and drawn tokens
   PinnedBuffer pin, pin_out;
@@ -447,6 +446,7 @@ struct pia_model {
   // through a cached graph for `key` (decode steps, replayed every step).
   template <typename F>
   void run_step(const std::array<int64_t, 6>& key, bool replay, F&& body) {
+    if (!replay_graphs) replay = false;
     if (!replay && !prof.on) {
       body();
       return;
@@ -609,6 +609,7 @@ pia_status pia_model_create(pia_context* ctx, const pia_model_config* cfg, pia_m
   if (const char* e = std::getenv("PIA_MFMA_MIN_BATCH")) m->mfma_min = std::max<int64_t>(2, std::atoll(e));
   // Diagnostic: PIA_DEC_SPLIT=0 turns the decode GEMM's split K off.
   if (const char* e = std::getenv("PIA_DEC_SPLIT")) m->dec_split_on = std::atoi(e) != 0;
+  if (const char* e = std::getenv("PIA_NO_GRAPH")) m->replay_graphs = std::atoi(e) == 0;
   *out = m;
   PIA_API_END
 }

@@ -145,6 +145,33 @@ void sample_with_context(pia_context* ctx, int32_t* out, const float* logits, in
   }
   launch_sample(logits, ld, n, vocab, params, rng_state, out, mode, ctx->sample_ws.ptr, ctx->sample_ws.bytes, st);
 }
+void launch_projection(pia_context* ctx, const GemvArgs& g, hipStream_t st) {
+  const bool a16 = (reinterpret_cast<uintptr_t>(g.W) & 15) == 0 && (reinterpret_cast<uintptr_t>(g.x) & 15) == 0;
+  if (!(g.wkind == 1 && g.batch >= kMfmaMinBatch && g.cols % 64 == 0 && g.ldw % 64 == 0 && g.ldx % 4 == 0 && a16 &&
+        g.norm_w == nullptr && g.amax == nullptr && g.scales != nullptr)) {
+    launch_gemv(g, st);
+    return;
+  }
+  PIA_REQUIRE(g.rows > 0 && g.rows < (int64_t(1) << 31) && g.batch < (int64_t(1) << 31) && g.cols < (int64_t(1) << 30),
+              "projection: shape exceeds int32 indexing");
+  constexpr int64_t kSplitTiles = 255;
+  const size_t dig = xdigits_bytes(g.batch, g.cols), split = dec_split_bytes(kSplitTiles);
+  if (ctx->proj_digits.bytes < dig || ctx->proj_split.bytes < split) {
+    PIA_HIP(hipDeviceSynchronize());  // the old workspace may still be in use by queued work
+    ctx->proj_digits.ensure(dig);
+    if (ctx->proj_split.bytes < split) {
+      ctx->proj_split.ensure(split);
+      PIA_HIP(hipMemset(ctx->proj_split.ptr, 0, split));  // every launch leaves the counters zero
+    }
+  }
+  const DecSplitWork sw{ctx->proj_split.as<unsigned long long>(),
+                        reinterpret_cast<unsigned*>(ctx->proj_split.as<char>() + kSplitTiles * 8 * 16 * 64 * 8),
+                        kSplitTiles};
+  launch_xdigits(g.x, g.ldx, nullptr, 0.0f, g.batch, g.cols, ctx->proj_digits.ptr, st);
+  launch_gemm_i8_mfma(static_cast<const int8_t*>(g.W), g.ldw, g.scales, ctx->proj_digits.ptr, g.out, g.osb, g.osr,
+                      g.rows, g.cols, g.batch, g.epi, nullptr, &sw, st);
+}
+
 }  // namespace pia
 
 extern "C" {
@@ -253,8 +280,8 @@ pia_status pia_matvec_i8_dev(pia_context* ctx, float* out, const float* x, const
                              int64_t rows, int64_t cols, void* stream) {
   PIA_API_BEGIN
   PIA_REQUIRE(ctx && out && x && w && scales, "null argument");
-  launch_gemv(GemvArgs{1, w, cols, scales, x, cols, nullptr, 0.f, out, 0, 1, rows, cols, 1, Epi::Store},
-              stream_of(ctx, stream));
+  launch_projection(ctx, GemvArgs{1, w, cols, scales, x, cols, nullptr, 0.f, out, 0, 1, rows, cols, 1, Epi::Store},
+                    stream_of(ctx, stream));
   PIA_API_END
 }
 
@@ -262,8 +289,9 @@ pia_status pia_matmat_i8_dev(pia_context* ctx, float* out_rb, const float* x_br,
                              const float* scales, int64_t batch, int64_t rows, int64_t cols, void* stream) {
   PIA_API_BEGIN
   PIA_REQUIRE(ctx && out_rb && x_br && w && scales, "null argument");
-  launch_gemv(GemvArgs{1, w, cols, scales, x_br, cols, nullptr, 0.f, out_rb, 1, batch, rows, cols, batch, Epi::Store},
-              stream_of(ctx, stream));
+  launch_projection(ctx, GemvArgs{1, w, cols, scales, x_br, cols, nullptr, 0.f, out_rb, 1, batch, rows, cols, batch,
+                                  Epi::Store},
+                    stream_of(ctx, stream));
   PIA_API_END
 }
 
@@ -271,8 +299,9 @@ pia_status pia_qlinear_apply_dev(pia_context* ctx, float* out_br, const float* x
                                  const float* scales, int64_t batch, int64_t rows, int64_t cols, void* stream) {
   PIA_API_BEGIN
   PIA_REQUIRE(ctx && out_br && x_br && w && scales, "null argument");
-  launch_gemv(GemvArgs{1, w, cols, scales, x_br, cols, nullptr, 0.f, out_br, rows, 1, rows, cols, batch, Epi::Store},
-              stream_of(ctx, stream));
+  launch_projection(ctx, GemvArgs{1, w, cols, scales, x_br, cols, nullptr, 0.f, out_br, rows, 1, rows, cols, batch,
+                                  Epi::Store},
+                    stream_of(ctx, stream));
   PIA_API_END
 }
 
@@ -299,9 +328,10 @@ pia_status host_projection(pia_context* ctx, float* out, const float* x_br, cons
   PIA_HIP(hipMemcpyAsync(dw.ptr, w, rows * cols, hipMemcpyHostToDevice, st));
   PIA_HIP(hipMemcpyAsync(ds.ptr, scales, rows * sizeof(float), hipMemcpyHostToDevice, st));
   PIA_HIP(hipMemcpyAsync(dx.ptr, x_br, batch * cols * sizeof(float), hipMemcpyHostToDevice, st));
-  launch_gemv(GemvArgs{1, dw.ptr, cols, static_cast<const float*>(ds.ptr), static_cast<const float*>(dx.ptr), cols,
-                       nullptr, 0.f, static_cast<float*>(dout.ptr), osb, osr, rows, cols, batch, Epi::Store},
-              st);
+  launch_projection(ctx,
+                    GemvArgs{1, dw.ptr, cols, static_cast<const float*>(ds.ptr), static_cast<const float*>(dx.ptr),
+                             cols, nullptr, 0.f, static_cast<float*>(dout.ptr), osb, osr, rows, cols, batch, Epi::Store},
+                    st);
   PIA_HIP(hipMemcpyAsync(out, dout.ptr, batch * rows * sizeof(float), hipMemcpyDeviceToHost, st));
   PIA_HIP(hipStreamSynchronize(st));
   PIA_API_END
@@ -421,7 +451,8 @@ pia_status pia_bench_projection(pia_context* ctx, int64_t rows, int64_t cols, in
   auto one = [&](int i) {
     const int8_t* wi = static_cast<int8_t*>(w.ptr) + (i % ncopy) * wbytes;
     if (flags & 8) {
-      launch_xdigits(x.as<float>(), ldx, norm, 1e-5f, batch, cols, xq.ptr, st);
+      // flags & 16: the digits are written once before the timed launches (projection alone).
+      if (!(flags & 16) || i == 0) launch_xdigits(x.as<float>(), ldx, norm, 1e-5f, batch, cols, xq.ptr, st);
       launch_gemm_i8_mfma(wi, ldw, s.as<float>(), xq.ptr, y.as<float>(), rows, 1, rows, cols, batch, epi, nullptr,
                           &split, st);
     } else {

@@ -15,6 +15,9 @@ namespace pia {
 // thousands of workgroups from serializing on one.
 constexpr int kArgmaxSlots = 256;
 
+// Batch from which int8 projections run on the matrix cores instead of the streaming GEMV.
+constexpr int64_t kMfmaMinBatch = 5;
+
 // Epilogue of a projection: store, accumulate into the destination (residual add, as
 // src/model.rs:1127-1129 and :1165-1167 do with proj_out / ff_down), or SwiGLU over
 // interleaved gate/up row pairs (src/math.rs:293-302).

@@ -509,6 +509,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
     // differently). S goes to Ps, then each thread reads its (row, token) elements.
     {
       constexpr int NTT = kPfChunk / 16;           // token tiles per chunk
+      static_assert(kThreads == 256, "the score tiles are split over exactly four waves");
       constexpr int TPW = (R / 16) * NTT / 4;      // tiles per wave
       constexpr int KL = HD / 4;                   // head dims per lane group
       static_assert(TPW >= 1 && (R / 16) * NTT % 4 == 0 && NTT % TPW == 0, "score tiles per wave");

@@ -1,0 +1,195 @@
+"""GPU parity at the two BASELINE configs the other model tests only reach in reduced form.
+
+a TinyLlama-shape 2048-token prefill (prefill_batched, src/model.rs:1222-1255) into
+a randomly permuted block table: last-position logits, argmax and every K/V row the prefill
+wrote are compared with the oracle, then greedy decode continues from that state.
+
+the Llama-3-8B shape at batch 64 with prefix sharing and copy-on-write
+(KvCacheManager::admit / publish / fork / ensure_writable / append_block,
+src/memory/kv_cache_manager.rs:116-327, then decode_batch_into, src/model.rs:1184-1207): block
+tables and COW counts bit-exact between the product manager and the oracle's restatement,
+greedy tokens and logits of the batch-64 decode vs the oracle.
+
+Layer counts are cut (2 layers) so the oracle finishes in seconds; every per-layer shape, the
+vocabulary, the block size and the batch are the configs' own. The KV history of configs[4] is
+synthetic (seeded, identical on both sides): the prefix prefill itself is what configs[3]
+checks.
+
+Bar: greedy tokens, block tables and COW counts bit-exact; logits
+within max|delta| <= 2e-3 of the logit scale; K/V rows within 1e-4 of the cache scale."""
+import numpy as np
+import pytest
+
+import pia
+from oracle import memory as om
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+LOGIT_TOL = 2e-3
+KV_TOL = 1e-4
+
+
+def _rel(a, b):
+    return float(np.max(np.abs(a - b)) / max(1e-30, np.max(np.abs(b))))
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def test_config4_tinyllama_2048_token_prefill(ctx):
+    """TinyLlama shapes (hidden 2048, 32/4 heads, FFN 5632, vocab 32000),
+    2 layers, one 2048-token uniform-random prompt prefilled in one call (the LDS-tiled matrix-core
+    GEMM and the query-tiled prefill attention), blocks from a random permutation of the pool;
+    then 4 greedy decode steps on the KV state the prefill left."""
+    base = pia.TINYLLAMA
+    cfg = pia.LlamaConfig(hidden=base.hidden, layers=2, heads=base.heads, kv_heads=base.kv_heads,
+                          inter=base.inter, vocab=base.vocab)
+    n, bs, steps = 2048, 16, 4
+    rng = np.random.default_rng(3003)
+    nb = (n + steps + bs - 1) // bs + 3
+    table = rng.permutation(nb).tolist()
+    prompt = rng.integers(0, cfg.vocab, n).tolist()
+    _say(f"[config4-prefill] n={n} blocks={nb}: building weights")
+    w = pia.synth_weights(cfg, seed=3003)
+    gm = pia.Model(ctx, cfg, w)
+    gm.kv_alloc(nb, bs)
+    om_ = orc.OracleModel(cfg, w)
+    kv = np.zeros(orc.kv_floats(cfg, nb, bs), np.float32)
+    _say("[config4-prefill] GPU prefill")
+    lg, tg = gm.prefill(prompt, 0, table)
+    _say("[config4-prefill] oracle prefill")
+    lc = om_.prefill(prompt, 0, table, kv, nb, bs)
+    rel = _rel(lg, lc)
+    _say(f"[config4-prefill] rel max|dlogit|={rel:.3g} argmax gpu={tg} cpu={orc.argmax(lc)}")
+    assert tg == orc.argmax(lc)
+    assert rel <= LOGIT_TOL
+    # Every slot the prefill wrote (positions 0..n-1 through the permuted table) agrees; the
+    # slots it did not write are still zero on both sides.
+    got = gm.kv_download().reshape(cfg.layers, nb * bs, -1)
+    ref = kv.reshape(cfg.layers, nb * bs, -1)
+    written = np.zeros(nb * bs, bool)
+    for p in range(n):
+        written[table[p // bs] * bs + p % bs] = True
+    assert np.all(got[:, ~written] == 0) and np.all(ref[:, ~written] == 0)
+    scale = float(np.max(np.abs(ref[:, written])))
+    kv_err = float(np.max(np.abs(got[:, written] - ref[:, written])))
+    _say(f"[config4-prefill] K/V max|delta|={kv_err:.3g} (scale {scale:.3g})")
+    assert kv_err <= KV_TOL * scale
+    # Greedy decode continues on the prefilled state (each side on its own cache).
+    tok_g = tok_c = tg
+    for i in range(steps):
+        lg, am = gm.decode([tok_g], [n + i], [table])
+        lc = om_.decode([tok_c], [n + i], [table], kv, nb, bs)
+        r = _rel(lg[0], lc[0])
+        tok_g, tok_c = int(am[0]), orc.argmax(lc[0])
+        _say(f"[config4-prefill] decode step {i}: rel={r:.3g} token {tok_g}/{tok_c}")
+        assert tok_g == tok_c and r <= LOGIT_TOL
+    gm.close()
+
+
+def test_config5_llama3_batch64_prefix_sharing_cow(ctx):
+    """BASELINE configs[4] workload at the Llama-3-8B shape (hidden 4096, 32/8 heads, head_dim
+    128, FFN 14336, vocab 128256, rotary theta 500000), 2 layers: 4 random 1024-token prefixes,
+    each admitted by 8 parent sequences (+ an 8-token tail) through the PrefixCache (the first
+    misses and publishes, the other 7 hit); every parent forks 2 children that share its
+    partially filled tail block; each child's first write at position 1032 copies that block
+    (copy-on-write on the device), its blocks are appended up to its 256 unique tokens and the
+    decode steps; the parents are released. The 64 children then decode 3 greedy steps at
+    batch 64 from position 1288."""
+    cfg = pia.LlamaConfig(hidden=4096, layers=2, heads=32, kv_heads=8, inter=14336, vocab=128256,
+                          rope_theta=500000.0)
+    bs, groups, parents, kids, prefix_len, tail_len, uniq, steps = 16, 4, 8, 2, 1024, 8, 256, 3
+    prompt_total = prefix_len + tail_len + uniq
+    n_child = groups * parents * kids
+    per_child = (prompt_total + steps + bs - 1) // bs - prefix_len // bs
+    total = groups * (prefix_len // bs + parents) + n_child * per_child + 8
+    rng = np.random.default_rng(5005)
+    _say(f"[config5] pool of {total} blocks: building weights")
+    w = pia.synth_weights(cfg, seed=5005)
+    gm = pia.Model(ctx, cfg, w)
+    gm.kv_alloc(total, bs)
+    kv = rng.standard_normal(orc.kv_floats(cfg, total, bs), dtype=np.float32) * 0.5
+    gm.kv_upload(kv)
+    olay = om.KvLayout(cfg.layers, total, bs, cfg.kv_heads, cfg.head_dim)
+    mg, mo = pia.KvCacheManager(total, bs), om.KvCacheManager(total, bs)
+    tick = 0
+    children = []  # (seq_id, product table, oracle table)
+    parent_ids = []
+    for g in range(groups):
+        prefix = rng.integers(0, cfg.vocab, prefix_len).tolist()
+        for p in range(parents):
+            pid = 1000 + g * parents + p
+            toks = prefix + rng.integers(0, cfg.vocab, tail_len).tolist()
+            tick += 1
+            got = mg.admit(pid, toks, tick)
+            ao = mo.admit(pid, toks, tick)
+            assert got is not None and ao is not None
+            tg, info = got
+            assert tg.blocks() == ao.table.blocks()
+            assert info[0] == ao.cached_tokens == (0 if p == 0 else prefix_len)
+            assert mg.publish(tg) == mo.publish_prompt_blocks(ao.table)
+            parent_ids.append(pid)
+            for k in range(kids):
+                cid = (g * parents + p) * kids + k
+                tick += 1
+                cg, co = mg.fork(tg, cid, tick), mo.fork(ao.table, cid, tick)
+                assert cg.blocks() == co.blocks()
+                children.append((cid, cg, co))
+    # First write of each child: copy-on-write of the shared tail block, then its own blocks.
+    pos0 = prefix_len + tail_len
+    for cid, cg, co in children:
+        c1 = mg.ensure_writable(cid, cg, pos0, ctx, gm.kv_ptr, gm.layout)
+        c2 = mo.ensure_writable(cid, co, pos0, lambda a, b: olay.copy_block(kv, a, b))
+        assert c1 == c2
+        while len(cg) * bs < prompt_total + steps:
+            tick += 1
+            assert mg.append_block(cid, cg, tick) == mo.append_block(cid, co, tick)
+        assert cg.blocks() == co.blocks()
+    for pid in parent_ids:
+        mg.release(pid)
+        mo.release_sequence(pid)
+    st = mg.stats()
+    _say(f"[config5] manager stats {st}")
+    assert st["cow_copies"] == mo.cow_copies == n_child
+    assert st["hits"] == mo.cache.hits and st["misses"] == mo.cache.misses
+    assert st["hits"] == groups * (parents - 1) * (prefix_len // bs)
+    # Children of one group share the prefix blocks; every block's reference count agrees.
+    tables = [cg.blocks() for _, cg, _ in children]
+    for g in range(groups):
+        grp = tables[g * parents * kids:(g + 1) * parents * kids]
+        assert all(t[:prefix_len // bs] == grp[0][:prefix_len // bs] for t in grp)
+        assert len({t[prefix_len // bs] for t in grp}) == parents * kids  # private tails after COW
+    for b in sorted({b for t in tables for b in t}):
+        assert mg.ref_count(b) == mo.alloc.ref_count(b)
+    # The device copy-on-write moved the same bytes as the oracle's copy_block.
+    got = gm.kv_download()
+    assert np.array_equal(got, kv)
+    om_ = orc.OracleModel(cfg, w)
+    toks_g = rng.integers(0, cfg.vocab, n_child).tolist()
+    toks_c = list(toks_g)
+    for s in range(steps):
+        pos = [prompt_total + s] * n_child
+        _say(f"[config5] step {s}: GPU decode")
+        lg, am = gm.decode(toks_g, pos, tables)
+        _say(f"[config5] step {s}: oracle decode")
+        lc = om_.decode(toks_c, pos, tables, kv, total, bs)
+        rel = max(_rel(lg[b], lc[b]) for b in range(n_child))
+        toks_g = am.tolist()
+        toks_c = [orc.argmax(r) for r in lc]
+        mism = sum(int(a != b) for a, b in zip(toks_g, toks_c))
+        _say(f"[config5] step {s}: rel max|dlogit|={rel:.3g} argmax mismatches={mism}")
+        assert mism == 0
+        assert rel <= LOGIT_TOL
+    # Decode writes landed in each child's own blocks; every other slot is unchanged.
+    got = gm.kv_download().reshape(cfg.layers, total * bs, -1)
+    ref = kv.reshape(cfg.layers, total * bs, -1)
+    written = np.zeros(total * bs, bool)
+    for t in tables:
+        for s in range(steps):
+            p = prompt_total + s
+            written[t[p // bs] * bs + p % bs] = True
+    assert written.sum() == n_child * steps
+    assert np.array_equal(got[:, ~written], ref[:, ~written])
+    assert np.max(np.abs(got[:, written] - ref[:, written])) <= KV_TOL * np.max(np.abs(ref))
+    gm.close()

@@ -186,3 +186,64 @@ def test_argmax_ties_total_order(ctx):
         pia.check(pia.lib().pia_argmax_dev(ctx.h, out.ptr, d.ptr, logits.shape[0], logits.shape[1], None))
         ctx.sync()
         assert out.numpy().tolist() == [orc.argmax(r) for r in logits]
+
+
+def _outlier_case(rng, rows, cols, batch):
+    """Activations N(0,1) with channels scaled by 100 and 1000 (the outlier channels of real
+    Llama activations), weight rows N(0, 0.02) quantized, and the first 16 rows built to
+    expose a fixed-point image tied to the row maximum: zero weights on the outlier channels,
+    maximal (+-127) weights everywhere else."""
+    x = rng.normal(0, 1, (batch, cols)).astype(np.float32)
+    big100 = rng.choice(cols, 3, replace=False)
+    big1000 = rng.choice(np.setdiff1d(np.arange(cols), big100), 2, replace=False)
+    x[:, big100] *= 100.0
+    x[:, big1000] *= 1000.0
+    w = rng.normal(0, 0.02, (rows, cols)).astype(np.float32)
+    q, s = pia.quantize_rows_i8(w)
+    q[:16] = np.where(rng.random((16, cols)) < 0.5, -127, 127).astype(np.int8)
+    q[:16, big100] = 0
+    q[:16, big1000] = 0
+    s[:16] = np.float32(0.02 / 127)
+    return q, s, x
+
+
+def _digit_bound(q, s, x):
+    """Error bound of the matrix-core projection: each activation row b is rounded to the
+    fixed-point grid 2^(e_b - 22), max|x_b| < 2^e_b (|error| <= 2^(e_b - 23) per element); the
+    integer dot is exact; the int64 -> f32 conversion and the scale multiply round twice."""
+    m = np.max(np.abs(x.astype(np.float64)), axis=1)
+    e = np.frexp(m)[1].astype(np.float64)  # m = f * 2^e, f in [0.5, 1)
+    grid = np.ldexp(1.0, (e - 23).astype(np.int64))  # half a grid step, per batch row
+    qa = np.abs(q.astype(np.float64))
+    exact = (x.astype(np.float64) @ q.astype(np.float64).T) * s.astype(np.float64)[None, :]
+    bound = (grid[:, None] * (qa.sum(axis=1)[None, :] * s.astype(np.float64)[None, :])) * (1 + 2.0 ** -20)
+    return exact, bound + 2.0 ** -22 * np.abs(exact) + 1e-30
+
+
+@pytest.mark.parametrize("rows,cols,batch", [(512, 2048, 8), (4096, 4096, 32), (256, 14336, 64)])
+def test_digit_split_outlier_activations(ctx, rows, cols, batch):
+    """The int8 matrix-core projection (three 8-bit digits of a 23-bit fixed-point image of each
+    activation row) on rows with 100x and 1000x outlier channels: within its stated bound of the
+    exact (f64) projection, and within that bound plus the oracle's f32 bound of the
+    oracle (src/simd.rs:228-262 accumulation order)."""
+    print(f"[digits-outlier] rows={rows} cols={cols} batch={batch}", flush=True)
+    rng = np.random.default_rng(rows + cols + batch)
+    q, s, x = _outlier_case(rng, rows, cols, batch)
+    dq, ds, dx = ctx.to_device(q), ctx.to_device(s), ctx.to_device(x)
+    out = ctx.empty((batch, rows), np.float32)
+    pia.check(pia.lib().pia_qlinear_apply_dev(ctx.h, out.ptr, dx.ptr, dq.ptr, ds.ptr, batch, rows, cols, None))
+    ctx.sync()
+    got = out.numpy().astype(np.float64)
+    exact, bound = _digit_bound(q, s, x)
+    err = np.abs(got - exact)
+    assert np.all(err <= bound), float(np.max(err / bound))
+    ref = orc.matmat_i8(q, s, x).T.astype(np.float64)  # [batch][row]
+    ref_bound = _proj_bound(q, s, x)
+    assert np.all(np.abs(got - ref) <= bound + ref_bound)
+    # How the two errors compare on the rows built against the fixed-point image, relative to
+    # the scale of those outputs: far inside the logit tolerance (2e-3) the model is held to.
+    scale = float(np.max(np.abs(exact[:, :16])))
+    rel = float(np.max(err[:, :16])) / scale
+    rel_ref = float(np.max(np.abs(ref - exact)[:, :16])) / scale
+    print(f"[digits-outlier] max rel error: matrix cores {rel:.3g}, oracle f32 {rel_ref:.3g}", flush=True)
+    assert rel < 1e-3

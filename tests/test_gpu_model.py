@@ -151,6 +151,7 @@ PREFILL_ATTN = [  # hidden, heads, kv_heads, window, prompt tokens, resume split
     (256, 4, 4, 45, 130, 0),      # one head per kv head, sliding window of 45
     (512, 4, 2, None, 100, 0),    # head_dim 128
     (1024, 8, 4, 70, 160, 64),    # head_dim 128, window, resumed prefill
+    (1024, 16, 1, None, 150, 0),  # head_dim 64, 16 heads per kv head (two positions per tile)
 ]
 
 
@@ -396,3 +397,43 @@ def test_tinyllama_small_batch_decode(ctx, batch):
     assert am.tolist() == [orc.argmax(r) for r in lc]
     gm.close()
 
+
+
+def test_outlier_channels_batched_decode(ctx):
+    """Decode at batch 8 (int8 matrix-core projections on digit-split activations) of a model
+    whose RMSNorm weights carry 100x and 1000x channels, so every normalized activation row has
+    outliers: logits and greedy tokens vs the oracle."""
+    cfg = pia.LlamaConfig(hidden=512, layers=2, heads=8, kv_heads=2, inter=1024, vocab=2048)
+    w = pia.synth_weights(cfg, seed=91)
+    rng = np.random.default_rng(91)
+    for lw in w["layers"]:
+        for name in ("attn_norm", "ffn_norm"):
+            ch = rng.choice(cfg.hidden, 5, replace=False)
+            lw[name][ch[:3]] = 100.0
+            lw[name][ch[3:]] = 1000.0
+    batch, bs = 8, 16
+    ctxs = rng.integers(20, 120, batch)
+    need = [(int(c) + 4 + bs - 1) // bs for c in ctxs]
+    nb = sum(need)
+    perm = rng.permutation(nb).tolist()
+    tables, k = [], 0
+    for n in need:
+        tables.append(perm[k:k + n])
+        k += n
+    kv = (rng.standard_normal(orc.kv_floats(cfg, nb, bs), dtype=np.float32) * 0.5)
+    gm = pia.Model(ctx, cfg, w)
+    gm.kv_alloc(nb, bs)
+    gm.kv_upload(kv)
+    om_ = orc.OracleModel(cfg, w)
+    toks_g = rng.integers(0, cfg.vocab, batch).tolist()
+    toks_c = list(toks_g)
+    for s in range(3):
+        pos = [int(c) + s for c in ctxs]
+        lg, am = gm.decode(toks_g, pos, tables)
+        lc = om_.decode(toks_c, pos, tables, kv, nb, bs)
+        rel = max(_rel(lg[b], lc[b]) for b in range(batch))
+        print(f"[outlier model] step {s} rel={rel:.3g}", flush=True)
+        assert rel <= LOGIT_TOL
+        toks_g, toks_c = am.tolist(), [orc.argmax(r) for r in lc]
+        assert toks_g == toks_c
+    gm.close()
