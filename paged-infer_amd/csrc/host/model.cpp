@@ -25,8 +25,6 @@ inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
 // Rows up to which RMSNorm is fused into the projection that consumes it.
 constexpr int64_t kFusedNormRows = 64;
-// 16-row tiles the decode GEMM's split-K workspace covers (255 tiles x 8 slices x 8 KiB).
-constexpr int64_t kDecSplitTiles = 255;
 
 struct Proj {
   int kind = -1;  // -1 unset, 0 f32, 1 int8
@@ -161,8 +159,8 @@ struct pia_model {
     grow(amax, c * kArgmaxSlots * 8);
     grow(xq, xdigits_bytes(c, std::max(cfg.hidden, cfg.inter)));
     if (!dec_split.ptr) {
-      dec_split.ensure(dec_split_bytes(kDecSplitTiles));
-      PIA_HIP(hipMemset(dec_split.ptr, 0, dec_split_bytes(kDecSplitTiles)));  // launches leave it zero
+      dec_split.ensure(dec_split_bytes());
+      PIA_HIP(hipMemset(dec_split.ptr, 0, dec_split_bytes()));  // launches leave it zero
     }
     cap = c;
   }
@@ -230,9 +228,7 @@ struct pia_model {
       timed(6, 0, [&] { launch_xdigits(x_in, ldx, norm_w, cfg.rms_eps, batch, p.cols, xq.ptr, st()); });
       hipEvent_t b = nullptr;
       begin(cls, proj_bytes(p, batch, epi), &b);
-      const DecSplitWork split{dec_split.as<unsigned long long>(),
-                               reinterpret_cast<unsigned*>(dec_split.as<char>() + kDecSplitTiles * 8 * 16 * 64 * 8),
-                               kDecSplitTiles};
+      const DecSplitWork split = dec_split_work(dec_split.ptr);
       launch_gemm_i8_mfma(static_cast<const int8_t*>(p.w.ptr), p.ld, p.s.as<float>(), xq.ptr, out, ldo, 1, p.rows,
                           p.cols, batch, epi, amax_out, dec_split_on ? &split : nullptr, st());
       end(b);

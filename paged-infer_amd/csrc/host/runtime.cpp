@@ -154,8 +154,7 @@ void launch_projection(pia_context* ctx, const GemvArgs& g, hipStream_t st) {
   }
   PIA_REQUIRE(g.rows > 0 && g.rows < (int64_t(1) << 31) && g.batch < (int64_t(1) << 31) && g.cols < (int64_t(1) << 30),
               "projection: shape exceeds int32 indexing");
-  constexpr int64_t kSplitTiles = 255;
-  const size_t dig = xdigits_bytes(g.batch, g.cols), split = dec_split_bytes(kSplitTiles);
+  const size_t dig = xdigits_bytes(g.batch, g.cols), split = dec_split_bytes();
   if (ctx->proj_digits.bytes < dig || ctx->proj_split.bytes < split) {
     PIA_HIP(hipDeviceSynchronize());  // the old workspace may still be in use by queued work
     ctx->proj_digits.ensure(dig);
@@ -164,9 +163,7 @@ void launch_projection(pia_context* ctx, const GemvArgs& g, hipStream_t st) {
       PIA_HIP(hipMemset(ctx->proj_split.ptr, 0, split));  // every launch leaves the counters zero
     }
   }
-  const DecSplitWork sw{ctx->proj_split.as<unsigned long long>(),
-                        reinterpret_cast<unsigned*>(ctx->proj_split.as<char>() + kSplitTiles * 8 * 16 * 64 * 8),
-                        kSplitTiles};
+  const DecSplitWork sw = dec_split_work(ctx->proj_split.ptr);
   launch_xdigits(g.x, g.ldx, nullptr, 0.0f, g.batch, g.cols, ctx->proj_digits.ptr, st);
   launch_gemm_i8_mfma(static_cast<const int8_t*>(g.W), g.ldw, g.scales, ctx->proj_digits.ptr, g.out, g.osb, g.osr,
                       g.rows, g.cols, g.batch, g.epi, nullptr, &sw, st);
@@ -427,12 +424,10 @@ pia_status pia_bench_projection(pia_context* ctx, int64_t rows, int64_t cols, in
   y.ensure(batch * rows * 4);
   nw.ensure(ldx * 4);
   xq.ensure(xdigits_bytes(batch, cols));
-  constexpr int64_t kSplitTiles = 255;
   DeviceBuffer split_buf;
-  split_buf.ensure(dec_split_bytes(kSplitTiles));
-  PIA_HIP(hipMemset(split_buf.ptr, 0, dec_split_bytes(kSplitTiles)));
-  const DecSplitWork split{split_buf.as<unsigned long long>(),
-                           reinterpret_cast<unsigned*>(split_buf.as<char>() + kSplitTiles * 8 * 16 * 64 * 8), kSplitTiles};
+  split_buf.ensure(dec_split_bytes());
+  PIA_HIP(hipMemset(split_buf.ptr, 0, dec_split_bytes()));
+  const DecSplitWork split = dec_split_work(split_buf.ptr);
   {
     std::vector<int8_t> hw(wbytes);
     for (size_t i = 0; i < hw.size(); ++i) hw[i] = static_cast<int8_t>((i * 2654435761u >> 13) % 255 - 127);

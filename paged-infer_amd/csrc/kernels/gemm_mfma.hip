@@ -8,9 +8,15 @@
 // into three signed base-256 digits, v = d0 + 256 d1 + 65536 d2. Each digit is an int8
 // column of the B operand, so one MFMA pass computes sum_k W[r][k] * d_j[b][k] for all three
 // digits exactly in int32. The epilogue recombines y = (C0 + 256 C1 + 65536 C2) * 2^(e_b-22)
-// * scale[r]. The only rounding is the fixed-point image of x (|error| <= 2^-23 max|x_b| per
-// element) and the final conversion -- tighter than an f32 accumulation of the same dot.
+// * scale[r]. The only rounding is the fixed-point image of x (|error| <= 2^(e_b - 23) per
+// element, max|x_b| < 2^e_b) and the final conversions. On rows without outliers that is
+// tighter than an f32 accumulation of the same dot; an entry whose row holds a channel 1000x
+// the others sees its small elements on a grid ~2^-12 of their size (tests bound both cases).
+//
+// Digit layout (every kernel here): batch entries in groups of 16; entry b's digit plane j is
+// digit row (3 (b / 16) + j) * 16 + b % 16 of the [48 * groups][kpad] digit matrix.
 #include <cmath>
+#include <cstdlib>
 
 #include <algorithm>
 
@@ -25,11 +31,17 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 // Whole 64-entry chunks from which the LDS-tiled kernel takes over (prefill sizes).
 constexpr int64_t kTileMinChunks = 4;
-// Workgroups a split-K decode launch aims for (batch 32: 256 beat 512, and 512 beat 1024).
+// Workgroups a split-K decode launch aims for.
 constexpr int64_t kDecTargetGroups = 256;
-constexpr int kDecMinSplitTiles = 3;        // digit column tiles (16 columns) needed to split
-constexpr int64_t kDecMinSteps = 8;        // 64-byte k-steps per slice, at least
+constexpr int64_t kDecMinSteps = 8;  // 64-byte k-steps per slice, at least
 constexpr int64_t kDecMaxSplit = 8;
+
+__host__ __device__ inline int digit_row(int b, int j) { return ((b >> 4) * 3 + j) * 16 + (b & 15); }
+// Byte offset of digit row n, column k in a digit matrix of nrows rows: k-step major (the 64
+// bytes of every row for one k-step are contiguous, so a k-step's digit tile is one block).
+__host__ __device__ inline int64_t digit_off(int64_t n, int64_t k, int64_t nrows) {
+  return ((k >> 6) * nrows + n) * 64 + (k & 63);
+}
 
 __device__ inline float block_reduce_sum(float v, float* red) {
 #pragma unroll
@@ -59,14 +71,14 @@ __device__ inline float block_reduce_max(float v, float* red) {
 // One workgroup per activation row b (rows >= batch write zero digits). Optional RMSNorm.
 __global__ __launch_bounds__(kThreads) void k_xdigits(const float* __restrict__ x, int64_t ldx,
                                                       const float* __restrict__ nw, float eps, int cols, int batch,
-                                                      int kpad, int8_t* __restrict__ dig, float* __restrict__ pow2) {
+                                                      int kpad, int nrows, int8_t* __restrict__ dig,
+                                                      float* __restrict__ pow2) {
   __shared__ float red[kThreads / 64];
   const int b = blockIdx.x;
-  int8_t* d0 = dig + static_cast<int64_t>(3 * b) * kpad;
-  int8_t* d1 = d0 + kpad;
-  int8_t* d2 = d1 + kpad;
+  const int n0 = digit_row(b, 0), n1 = digit_row(b, 1), n2 = digit_row(b, 2);
+  auto D = [&](int n, int k) -> int8_t& { return dig[digit_off(n, k, nrows)]; };
   if (b >= batch) {
-    for (int k = threadIdx.x; k < kpad; k += kThreads) d0[k] = d1[k] = d2[k] = 0;
+    for (int k = threadIdx.x; k < kpad; k += kThreads) D(n0, k) = D(n1, k) = D(n2, k) = 0;
     if (threadIdx.x == 0) pow2[b] = 0.0f;
     return;
   }
@@ -118,9 +130,9 @@ __global__ __launch_bounds__(kThreads) void k_xdigits(const float* __restrict__ 
     const int v1 = (v - a0) >> 8;
     const int a1 = ((v1 + 128) & 255) - 128;
     const int a2 = (v1 - a1) >> 8;  // |a2| <= 64
-    d0[k] = static_cast<int8_t>(a0);
-    d1[k] = static_cast<int8_t>(a1);
-    d2[k] = static_cast<int8_t>(a2);
+    D(n0, k) = static_cast<int8_t>(a0);
+    D(n1, k) = static_cast<int8_t>(a1);
+    D(n2, k) = static_cast<int8_t>(a2);
   };
   if (in_regs) {
 #pragma unroll
@@ -143,7 +155,7 @@ __global__ __launch_bounds__(kThreads) void k_xdigits(const float* __restrict__ 
 template <int kV4, int W>
 __global__ __launch_bounds__(256) void k_xdigits_wave(const float* __restrict__ x, int64_t ldx,
                                                       const float* __restrict__ nw, float eps, int cols, int batch,
-                                                      int groups, int kpad, int8_t* __restrict__ dig,
+                                                      int groups, int kpad, int nrows, int8_t* __restrict__ dig,
                                                       float* __restrict__ pow2) {
   // W wavefronts per row (4 / W rows per workgroup); the row's lanes are sub * 64 + lane.
   __shared__ float red[2][4];
@@ -153,16 +165,21 @@ __global__ __launch_bounds__(256) void k_xdigits_wave(const float* __restrict__ 
   const int b = blockIdx.x * (4 / W) + wave / W;
   const bool live = b < groups;
   const bool real = b < batch;
-  int* d0 = reinterpret_cast<int*>(dig + static_cast<int64_t>(3 * (live ? b : 0)) * kpad);
-  int* d1 = d0 + kpad / 4;
-  int* d2 = d1 + kpad / 4;
+  // Four digits per 32-bit store: float4 index i covers columns 4i .. 4i + 3 of one k-step.
+  const int bb0 = live ? b : 0;
+  const int n0 = digit_row(bb0, 0), n1 = digit_row(bb0, 1), n2 = digit_row(bb0, 2);
+  int* dw = reinterpret_cast<int*>(dig);
+  auto at = [&](int n, int i) -> int& { return dw[digit_off(n, 4 * i, nrows) >> 2]; };
   const int n4 = cols >> 2, kp4 = kpad >> 2;
   const float4* x4 = reinterpret_cast<const float4*>(x + static_cast<int64_t>(real ? b : 0) * ldx);
-  float4 v[kV4];
+  float4 v[kV4], nv[kV4];
+  const float4* w4 = reinterpret_cast<const float4*>(nw);
 #pragma unroll
   for (int u = 0; u < kV4; ++u) {
     const int i = rl + 64 * W * u;
     v[u] = (real && i < n4) ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    // The norm weights are loaded with the row (not after the reduction): one memory round trip.
+    if (nw) nv[u] = (real && i < n4) ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   // Row sum over the W waves: wave shuffle, then the partials through LDS.
   auto row_reduce = [&](float t, int slot, bool is_max) {
@@ -180,7 +197,6 @@ __global__ __launch_bounds__(256) void k_xdigits_wave(const float* __restrict__ 
     return r;
   };
   if (nw) {
-    const float4* w4 = reinterpret_cast<const float4*>(nw);
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < kV4; ++u) ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
@@ -190,7 +206,7 @@ __global__ __launch_bounds__(256) void k_xdigits_wave(const float* __restrict__ 
     for (int u = 0; u < kV4; ++u) {
       const int i = rl + 64 * W * u;
       if (real && i < n4) {
-        const float4 w = w4[i];
+        const float4 w = nv[u];
         v[u] = make_float4((v[u].x * inv) * w.x, (v[u].y * inv) * w.y, (v[u].z * inv) * w.z, (v[u].w * inv) * w.w);
       }
     }
@@ -223,12 +239,12 @@ __global__ __launch_bounds__(256) void k_xdigits_wave(const float* __restrict__ 
       split(v[u].y, a[1], bb[1], c[1]);
       split(v[u].z, a[2], bb[2], c[2]);
       split(v[u].w, a[3], bb[3], c[3]);
-      d0[i] = pack(a[0], a[1], a[2], a[3]);
-      d1[i] = pack(bb[0], bb[1], bb[2], bb[3]);
-      d2[i] = pack(c[0], c[1], c[2], c[3]);
+      at(n0, i) = pack(a[0], a[1], a[2], a[3]);
+      at(n1, i) = pack(bb[0], bb[1], bb[2], bb[3]);
+      at(n2, i) = pack(c[0], c[1], c[2], c[3]);
     }
   }
-  for (int i = n4 + rl; i < kp4; i += 64 * W) d0[i] = d1[i] = d2[i] = 0;  // the k-step padding
+  for (int i = n4 + rl; i < kp4; i += 64 * W) at(n0, i) = at(n1, i) = at(n2, i) = 0;  // the k-step padding
   if (rl == 0) pow2[b] = real ? ldexpf(1.0f, -sh) : 0.0f;
 }
 
@@ -239,345 +255,330 @@ __device__ inline uint32_t order_key(float f) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// Decode GEMM: one workgroup per 16 weight rows x NT*16 digit columns (all of the batch's
-// digits for NT <= 12); the 4 wavefronts split K (interleaved 64-wide steps) and their int32
-// partial sums are added in LDS. Every weight byte is read once per launch.
+// Decode GEMM (batches of up to 64 entries per launch chunk): one workgroup per 64*RT weight rows
+// (wave w owns rows 16*RT*w .. +16*RT, RT 16-row operand tiles) x all 16*NT digit columns of the
+// chunk's entries, over one K slice (grid.z) of the 64-byte k-steps.
 //
-// Split K (gridDim.z > 1, for launches with fewer row tiles than CUs): workgroup z covers the
-// z-th slice of the k-steps and stores its exact partial sums c0 + 256 c1 + 65536 c2 in its
-// own 64-bit slots of the workspace `ws`; the last slice of a row tile to arrive adds the
-// slices in slice order (exact integers: the result does not depend on arrival order), runs
-// the epilogue and resets the tile's counter for the next launch.
-template <int NT, int EPI, bool AMAX>
-__global__ __launch_bounds__(kThreads) void k_gemm_dec(const int8_t* __restrict__ W, int64_t ldw,
-                                                       const float* __restrict__ S, const int8_t* __restrict__ D,
-                                                       int kpad, const float* __restrict__ pow2,
+// The weight stream is the HBM-bound part; the digits are small, shared by every workgroup and
+// L2-resident. Each k-step's weights (per wave) and digits (per workgroup, 16 bytes per thread)
+// are issued PD k-steps ahead into a register ring, so the in-order completion counter never
+// has to drain the weight stream to reach a digit load; a k-step's digits go to LDS one k-step
+// before use (double buffer, one barrier per k-step) and every wave reads them from there.
+//
+// Digit layout: entry b's digit j is digit row (3 (b / 16) + j) * 16 + b % 16, so in the
+// 16x16 result tiles 3g, 3g+1, 3g+2 lane l holds the three digit sums of entry 16g + l % 16
+// for rows 4 (l / 16) + v: the epilogue recombines c0 + 256 c1 + 65536 c2 in registers.
+//
+// Split K (gridDim.z > 1, short matrices): slice z stores its exact 64-bit sums in its own
+// workspace slots (agent-scope stores, completed before the counter increment); the last slice
+// of a row tile to arrive adds the slices in slice order (exact: the result does not depend on
+// the arrival order), runs the epilogue and resets the tile's counter for the next launch.
+namespace dec {
+constexpr int kPitch = 64 + 16;  // LDS bytes per digit row of one k-step (rows land on distinct banks)
+}  // namespace dec
+
+template <int NG, int RT, int PD, int EPI, bool AMAX>
+__global__ __launch_bounds__(kThreads, 2) void k_gemm_dec(const int8_t* __restrict__ W, int64_t ldw,
+                                                          const float* __restrict__ S, const int8_t* __restrict__ D,
+                                                          int kpad, int nrows, const float* __restrict__ pow2,
                                                        float* __restrict__ O, int64_t osb, int64_t osr, int rows,
                                                        int batch, unsigned long long* __restrict__ amax,
                                                        unsigned long long* __restrict__ ws,
                                                        unsigned* __restrict__ cnt) {
-  __shared__ int csum[4][16][NT * 16];
-  __shared__ long long tot[16][64];
+  constexpr int NT = 3 * NG, N = 16 * NT;
+  constexpr int DV = (N * 4 + kThreads - 1) / kThreads;  // 16-byte digit loads per thread per k-step
+  constexpr int kRows = 64 * RT;                          // weight rows per workgroup
+  __shared__ __align__(16) int8_t dl[2][N * dec::kPitch];
   __shared__ int last;
   __shared__ unsigned long long best[AMAX ? 64 : 1];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row0 = blockIdx.x * 16;
-  if (AMAX && threadIdx.x < 64) best[threadIdx.x] = 0ull;
-  // grid.y: chunk of `batch` entries (64 per chunk when there are several).
-  D += static_cast<int64_t>(blockIdx.y) * 3 * batch * kpad;
-  O += static_cast<int64_t>(blockIdx.y) * batch * osb;
-  pow2 += static_cast<int64_t>(blockIdx.y) * batch;
-  if (AMAX) amax += static_cast<int64_t>(blockIdx.y) * batch * kArgmaxSlots;
-  const int r_l = lane & 15, kg = lane >> 4;  // operand row / column within the tile, k group
-  const int8_t* wp = W + static_cast<int64_t>(min(row0 + r_l, rows - 1)) * ldw + kg * 16;
-  const int8_t* dp = D + static_cast<int64_t>(r_l) * kpad + kg * 16;
-  v4i acc[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = v4i{0, 0, 0, 0};
-  const int nsplit = gridDim.z;
-  const int per = (kpad / 64 + nsplit - 1) / nsplit;
-  const int ks0 = blockIdx.z * per, ksteps = min(kpad / 64, ks0 + per);
-  constexpr int kU = 4;  // k-steps per wave whose loads are in flight together
-  for (int s0 = ks0 + wave; s0 < ksteps; s0 += 4 * kU) {
-    v4i a[kU];
-    v4i bm[kU][NT];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int s = s0 + 4 * u;
-      if (s < ksteps) {
-        a[u] = *reinterpret_cast<const v4i*>(wp + s * 64);
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-          bm[u][t] = *reinterpret_cast<const v4i*>(dp + static_cast<int64_t>(t * 16) * kpad + s * 64);
-      } else {
-        a[u] = v4i{0, 0, 0, 0};
-#pragma unroll
-        for (int t = 0; t < NT; ++t) bm[u][t] = v4i{0, 0, 0, 0};
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kU; ++u)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], bm[u][t], acc[t], 0, 0, 0);
-  }
-  // 16x16 int32 result tile t: lane holds rows 4*(lane/16) + v, column lane % 16.
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) csum[wave][4 * kg + v][t * 16 + r_l] = acc[t][v];
-  __syncthreads();
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r_l = lane & 15, kq = lane >> 4;
+  const int wrow0 = blockIdx.x * kRows + wave * 16 * RT;  // this wave's first row
+  if (AMAX && tid < 64) best[tid] = 0ull;
+  // grid.y: chunk of 64 entries (192 digit rows, 64 pow2 values, 64 output columns).
+  D += static_cast<int64_t>(blockIdx.y) * 192 * 64;
+  const int64_t dstep = static_cast<int64_t>(nrows) * 64;  // bytes per k-step of the digit matrix
+  O += static_cast<int64_t>(blockIdx.y) * 64 * osb;
+  pow2 += static_cast<int64_t>(blockIdx.y) * 64;
+  if (AMAX) amax += static_cast<int64_t>(blockIdx.y) * 64 * kArgmaxSlots;
 
-  // This workgroup's sum for (tile row r, batch entry b); the three digit columns of b are
-  // 3b, 3b+1, 3b+2.
-  auto partial = [&](int r, int b) {
-    int64_t c[3];
+  const int8_t* wp[RT];
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      const int col = 3 * b + j;
-      c[j] = static_cast<int64_t>(csum[0][r][col]) + csum[1][r][col] + csum[2][r][col] + csum[3][r][col];
-    }
-    return c[0] + 256 * c[1] + 65536 * c[2];
+  for (int rt = 0; rt < RT; ++rt)
+    wp[rt] = W + static_cast<int64_t>(min(wrow0 + rt * 16 + r_l, rows - 1)) * ldw + kq * 16;
+  // Every load and LDS store below is unconditional (no lane-divergent branches, no skipped
+  // refills), so the compiler's wait counts see the same number of loads in flight on every
+  // path and keep the ring in flight. Threads past the digit tile repeat the last segment
+  // (same data to the same LDS bytes); refills past the slice re-read its last k-step.
+  const int8_t* dp[DV];
+  int doff[DV];
+#pragma unroll
+  for (int i = 0; i < DV; ++i) {
+    const int idx = min(tid + i * kThreads, N * 4 - 1);
+    const int n = idx >> 2, seg = idx & 3;
+    dp[i] = D + n * 64 + seg * 16;
+    doff[i] = n * dec::kPitch + seg * 16;
+  }
+
+  const int nsplit = gridDim.z;
+  const int ksteps = kpad / 64;
+  const int per = (ksteps + nsplit - 1) / nsplit;
+  const int c0 = blockIdx.z * per, c1 = min(ksteps, c0 + per);
+  // Workgroups start their slice at staggered k-steps (the integer sums do not depend on the
+  // order), so concurrent loads spread over the memory channels. Logical step c of the slice
+  // reads physical k-step c0 + (c - c0 + rot) mod len; refills past the slice repeat its last.
+  const int len = max(c1 - c0, 1);
+  const int rot = static_cast<int>((blockIdx.x * 5u) % static_cast<unsigned>(len));
+  auto phys = [&](int c) {
+    int j = min(c - c0, len - 1) + rot;
+    return c0 + (j >= len ? j - len : j);
   };
-  if (nsplit > 1) {
-    // Slot of slice z: ws[tile][z][16][64]; agent-scope stores, visible on every XCD once done.
-    const int64_t tile = static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
-    unsigned long long* wt = ws + tile * kDecMaxSplit * 16 * 64;
-    for (int idx = threadIdx.x; idx < 16 * batch; idx += kThreads) {
-      const int r = idx / batch, b = idx % batch;
-      __hip_atomic_store(wt + (static_cast<int64_t>(blockIdx.z) * 16 + r) * 64 + b,
-                         static_cast<unsigned long long>(partial(r, b)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  v4i wr[PD][RT], dr[PD][DV];
+  auto load_w = [&](int c, v4i (&w)[RT]) {
+    const int64_t off = static_cast<int64_t>(phys(c)) * 64;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) w[rt] = *reinterpret_cast<const v4i*>(wp[rt] + off);
+  };
+  auto load_d = [&](int c, v4i (&d)[DV]) {
+    const int64_t off = static_cast<int64_t>(phys(c)) * dstep;
+#pragma unroll
+    for (int i = 0; i < DV; ++i) d[i] = *reinterpret_cast<const v4i*>(dp[i] + off);
+  };
+  auto store_d = [&](int stage, const v4i (&d)[DV]) {
+#pragma unroll
+    for (int i = 0; i < DV; ++i) *reinterpret_cast<v4i*>(&dl[stage][doff[i]]) = d[i];
+  };
+
+  v4i acc[RT][NT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[rt][t] = v4i{0, 0, 0, 0};
+
+#pragma unroll
+  for (int i = 0; i < PD; ++i) load_w(c0 + i, wr[i]);
+#pragma unroll
+  for (int i = 0; i < PD; ++i) load_d(c0 + i, dr[i]);
+  store_d(0, dr[0]);
+  __syncthreads();
+  // One k-step: MFMAs on ring slot i (chunk c) and the LDS stage the previous step filled; then
+  // the next k-step's digits (loaded PD - 1 steps ago) into the other stage, which every wave
+  // finished reading before the previous barrier.
+  auto step = [&](int c, int i, const v4i (&w)[RT], const v4i (&dnext)[DV]) {
+    const int stage = (c - c0) & 1;
+    const int8_t* buf = dl[stage] + r_l * dec::kPitch + kq * 16;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const v4i b = *reinterpret_cast<const v4i*>(buf + t * 16 * dec::kPitch);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) acc[rt][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[rt], b, acc[rt][t], 0, 0, 0);
     }
-    // Waiting for the stores to complete (no cache writeback fence) orders them before the
-    // counter increment.
+    store_d(stage ^ 1, dnext);
+  };
+  // Whole groups of PD k-steps with no exit inside a group (an early exit would let the
+  // compiler sink the refills to their first use, serializing the stream), then the tail
+  // from the ring without refills.
+  int c = c0;
+  for (; c + PD <= c1; c += PD) {
+#pragma unroll
+    for (int i = 0; i < PD; ++i) {
+      step(c + i, i, wr[i], dr[(i + 1) % PD]);
+      load_w(c + i + PD, wr[i]);
+      load_d(c + i + PD, dr[i]);
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PD; ++i) {
+    if (c + i < c1) {
+      step(c + i, i, wr[i], dr[(i + 1) % PD]);
+      __syncthreads();
+    }
+  }
+
+  // Exact integer sum of entry b = 16 g + r_l for row 4 kq + v of tile rt.
+  auto digits_sum = [&](int rt, int g, int v) -> long long {
+    return static_cast<long long>(acc[rt][3 * g][v]) + 256ll * acc[rt][3 * g + 1][v] +
+           65536ll * acc[rt][3 * g + 2][v];
+  };
+  long long tot[RT][NG][4];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) tot[rt][g][v] = digits_sum(rt, g, v);
+
+  if (nsplit > 1) {
+    // Slots of pair (tile, z): [kRows rows][64 entries] 64-bit sums.
+    const int64_t tile = static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
+    unsigned long long* base = ws + tile * nsplit * kRows * 64;
+    const int lrow = wave * 16 * RT + kq * 4;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          __hip_atomic_store(base + (static_cast<int64_t>(blockIdx.z) * kRows + lrow + rt * 16 + v) * 64 + g * 16 + r_l,
+                             static_cast<unsigned long long>(tot[rt][g][v]), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    // Waiting for the stores to complete (no cache writeback) orders them before the counter
+    // increment; the last slice's agent-scope loads are issued only after it has seen the count.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (threadIdx.x == 0) {
-      unsigned* c = cnt + tile;
-      const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {
+      unsigned* cp = cnt + tile;
+      const unsigned old = __hip_atomic_fetch_add(cp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last = old == static_cast<unsigned>(nsplit - 1);
-      if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (last) __hip_atomic_store(cp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!last) return;
-    for (int idx = threadIdx.x; idx < 16 * batch; idx += kThreads) {
-      const int r = idx / batch, b = idx % batch;
-      long long t = 0;
-      for (int z = 0; z < nsplit; ++z)
-        t += static_cast<long long>(__hip_atomic_load(wt + (static_cast<int64_t>(z) * 16 + r) * 64 + b,
-                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-      tot[r][b] = t;
+    // Slice by slice (in slice order), every value of a slice loaded before any is added: one
+    // round trip per slice, not per value.
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) tot[rt][g][v] = 0;
+    for (int z = 0; z < nsplit; ++z) {
+      unsigned long long part[RT][NG][4];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            part[rt][g][v] = __hip_atomic_load(
+                base + (static_cast<int64_t>(z) * kRows + lrow + rt * 16 + v) * 64 + g * 16 + r_l, __ATOMIC_RELAXED,
+                __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) tot[rt][g][v] += static_cast<long long>(part[rt][g][v]);
     }
-    __syncthreads();
   }
-  auto total = [&](int r, int b) -> int64_t { return nsplit > 1 ? tot[r][b] : partial(r, b); };
 
-  // Epilogue: thread -> (row, batch entry).
-  for (int idx = threadIdx.x; idx < 16 * batch; idx += kThreads) {
-    const int r = idx / batch, b = idx % batch;
-    const int row = row0 + r;
-    const int64_t sum = total(r, b);
-    const float y = static_cast<float>(sum) * pow2[b];
-    if constexpr (EPI == kEpiSwiglu) {
-      if ((r & 1) == 0 && row + 1 < rows) {
-        const float yu = static_cast<float>(total(r + 1, b)) * pow2[b];
-        const float g = y * S[row];
-        const float u = yu * S[row + 1];
-        const float silu = g / (1.0f + expf(-g));
-        O[static_cast<int64_t>(b) * osb + static_cast<int64_t>(row >> 1) * osr] = silu * u;
+  // Epilogue: lane -> rows 4 kq + v of each tile, entries 16 g + r_l.
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    const int b = g * 16 + r_l;
+    const bool live = b < batch;
+    const float p2 = live ? pow2[b] : 0.0f;
+    unsigned long long mine = 0ull;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int rbase = wrow0 + rt * 16 + kq * 4;
+      if constexpr (EPI == kEpiSwiglu) {
+#pragma unroll
+        for (int v = 0; v < 4; v += 2) {
+          const int row = rbase + v;  // even: gate row, row + 1 the matching up row
+          if (live && row + 1 < rows) {
+            const float y = static_cast<float>(tot[rt][g][v]) * p2;
+            const float yu = static_cast<float>(tot[rt][g][v + 1]) * p2;
+            const float gt = y * S[row];
+            const float u = yu * S[row + 1];
+            const float silu = gt / (1.0f + expf(-gt));
+            O[static_cast<int64_t>(b) * osb + static_cast<int64_t>(row >> 1) * osr] = silu * u;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = rbase + v;
+          if (live && row < rows) {
+            const float val = static_cast<float>(tot[rt][g][v]) * p2 * S[row];
+            float* o = O + static_cast<int64_t>(b) * osb + static_cast<int64_t>(row) * osr;
+            if (EPI == kEpiAdd) *o = *o + val;
+            else *o = val;
+            if constexpr (AMAX) {
+              const unsigned long long cand =
+                  (static_cast<unsigned long long>(order_key(val)) << 32) | static_cast<uint32_t>(row);
+              mine = cand > mine ? cand : mine;
+            }
+          }
+        }
       }
-    } else if (row < rows) {
-      const float v = y * S[row];
-      float* o = O + static_cast<int64_t>(b) * osb + static_cast<int64_t>(row) * osr;
-      if (EPI == kEpiAdd) *o = *o + v;
-      else *o = v;
-      if constexpr (AMAX) {
-        const unsigned long long cand = (static_cast<unsigned long long>(order_key(v)) << 32) | static_cast<uint32_t>(row);
-        atomicMax(&best[b], cand);  // LDS: the 16 rows of this tile first
+    }
+    if constexpr (AMAX) {
+      // Lanes r_l, r_l + 16, r_l + 32, r_l + 48 hold the same entry: reduce them, then the waves
+      // of the workgroup in LDS.
+#pragma unroll
+      for (int off = 16; off < 64; off <<= 1) {
+        const unsigned long long o = __shfl_xor(mine, off, 64);
+        mine = o > mine ? o : mine;
       }
+      if (kq == 0 && live) atomicMax(&best[b], mine);
     }
   }
   if constexpr (AMAX) {
     __syncthreads();
-    // Then one atomic per batch entry and workgroup, spread over the slots.
-    if (threadIdx.x < batch)
-      atomicMax(&amax[threadIdx.x * kArgmaxSlots + (blockIdx.x & (kArgmaxSlots - 1))], best[threadIdx.x]);
+    if (tid < batch && tid < 64)
+      atomicMax(&amax[tid * kArgmaxSlots + (blockIdx.x & (kArgmaxSlots - 1))], best[tid]);
   }
 }
 
-// Tall-matrix decode GEMM: one workgroup per 64 weight rows (wave w owns rows 16w..16w+15 over
-// the full K) x NT*16 digit columns. The digit operand is staged once per workgroup in LDS, in
-// double-buffered KC-byte K chunks (row pitch padded by 16 bytes against bank conflicts). The
-// next chunk's weights and digits are loaded into registers before the current chunk's MFMAs
-// and written to LDS after them, so one memory round trip overlaps one chunk of compute.
-template <int NT>
-struct Rows64 {
-  static constexpr int kN = NT * 16;
-  static constexpr int kKC = NT <= 6 ? 512 : 256;          // bytes of K per stage
-  static constexpr int kPitch = kKC + 16;                  // LDS row pitch
-  static constexpr int kDig = kN * (kKC / 16) / kThreads;  // 16-byte digit loads per thread
-  static_assert(kN * (kKC / 16) % kThreads == 0, "digit tile must split evenly");
+// Choice of a decode launch: RT operand tiles per wave, K slices.
+struct DecPlan {
+  int rt, nsplit;
 };
 
-template <int NT, int EPI, bool AMAX>
-__global__ __launch_bounds__(kThreads) void k_gemm_rows64(const int8_t* __restrict__ W, int64_t ldw,
-                                                          const float* __restrict__ S, const int8_t* __restrict__ D,
-                                                          int kpad, const float* __restrict__ pow2,
-                                                          float* __restrict__ O, int64_t osb, int64_t osr, int rows,
-                                                          int batch, unsigned long long* __restrict__ amax) {
-  using T = Rows64<NT>;
-  constexpr int kN = T::kN, kKC = T::kKC, kPitch = T::kPitch, kDig = T::kDig, kU = kKC / 64;
-  extern __shared__ __align__(16) int8_t lds[];  // [2][kN][kPitch] digits; reused as int32 C [64][kN]
-  __shared__ unsigned long long best[AMAX ? 64 : 1];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row0 = blockIdx.x * 64;
-  D += static_cast<int64_t>(blockIdx.y) * 3 * batch * kpad;
-  O += static_cast<int64_t>(blockIdx.y) * batch * osb;
-  pow2 += static_cast<int64_t>(blockIdx.y) * batch;
-  if (AMAX) amax += static_cast<int64_t>(blockIdx.y) * batch * kArgmaxSlots;
-  if (AMAX && threadIdx.x < 64) best[threadIdx.x] = 0ull;
-  const int r_l = lane & 15, kg = lane >> 4;
-  const int8_t* wp = W + static_cast<int64_t>(min(row0 + wave * 16 + r_l, rows - 1)) * ldw + kg * 16;
-  const int nchunks = (kpad + kKC - 1) / kKC;
-
-  auto load_d = [&](int c, v4i (&d)[kDig]) {
-#pragma unroll
-    for (int i = 0; i < kDig; ++i) {
-      const int idx = threadIdx.x + i * kThreads;
-      const int n = idx / (kKC / 16), j = (idx % (kKC / 16)) * 16;
-      const int k = c * kKC + j;
-      d[i] = k < kpad ? *reinterpret_cast<const v4i*>(D + static_cast<int64_t>(n) * kpad + k) : v4i{0, 0, 0, 0};
-    }
-  };
-  auto store_d = [&](int c, const v4i (&d)[kDig]) {
-    int8_t* dst = lds + (c & 1) * kN * kPitch;
-#pragma unroll
-    for (int i = 0; i < kDig; ++i) {
-      const int idx = threadIdx.x + i * kThreads;
-      const int n = idx / (kKC / 16), j = (idx % (kKC / 16)) * 16;
-      *reinterpret_cast<v4i*>(dst + n * kPitch + j) = d[i];
-    }
-  };
-  auto load_w = [&](int c, v4i (&a)[kU]) {
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int k = c * kKC + u * 64;
-      a[u] = k < kpad ? *reinterpret_cast<const v4i*>(wp + k) : v4i{0, 0, 0, 0};
-    }
-  };
-
-  v4i acc[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = v4i{0, 0, 0, 0};
-  v4i a_cur[kU], a_next[kU], d_next[kDig];
-  load_w(0, a_cur);
-  load_d(0, d_next);
-  store_d(0, d_next);
-  __syncthreads();
-  for (int c = 0; c < nchunks; ++c) {
-    const bool more = c + 1 < nchunks;
-    if (more) {
-      load_w(c + 1, a_next);
-      load_d(c + 1, d_next);
-    }
-    const int8_t* buf = lds + (c & 1) * kN * kPitch;
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const v4i b = *reinterpret_cast<const v4i*>(buf + (t * 16 + r_l) * kPitch + u * 64 + kg * 16);
-        acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a_cur[u], b, acc[t], 0, 0, 0);
-      }
-    }
-    // Buffer (c + 1) & 1 was last read in iteration c - 1, before that iteration's barrier.
-    if (more) store_d(c + 1, d_next);
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < kU; ++u) a_cur[u] = a_next[u];
-  }
-
-  // C tile in LDS: [64 rows][kN] int32 (the digit buffers are no longer needed).
-  int* csum = reinterpret_cast<int*>(lds);
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) csum[(wave * 16 + 4 * kg + v) * kN + t * 16 + r_l] = acc[t][v];
-  __syncthreads();
-
-  for (int idx = threadIdx.x; idx < 64 * batch; idx += kThreads) {
-    const int r = idx / batch, b = idx % batch;
-    const int row = row0 + r;
-    const int* cr = csum + r * kN + 3 * b;
-    const int64_t sum = static_cast<int64_t>(cr[0]) + 256 * static_cast<int64_t>(cr[1]) + 65536 * static_cast<int64_t>(cr[2]);
-    const float y = static_cast<float>(sum) * pow2[b];
-    if constexpr (EPI == kEpiSwiglu) {
-      if ((r & 1) == 0 && row + 1 < rows) {
-        const int* cu = cr + kN;
-        const int64_t su = static_cast<int64_t>(cu[0]) + 256 * static_cast<int64_t>(cu[1]) + 65536 * static_cast<int64_t>(cu[2]);
-        const float yu = static_cast<float>(su) * pow2[b];
-        const float g = y * S[row];
-        const float u = yu * S[row + 1];
-        const float silu = g / (1.0f + expf(-g));
-        O[static_cast<int64_t>(b) * osb + static_cast<int64_t>(row >> 1) * osr] = silu * u;
-      }
-    } else if (row < rows) {
-      const float v = y * S[row];
-      float* o = O + static_cast<int64_t>(b) * osb + static_cast<int64_t>(row) * osr;
-      if (EPI == kEpiAdd) *o = *o + v;
-      else *o = v;
-      if constexpr (AMAX) {
-        const unsigned long long cand = (static_cast<unsigned long long>(order_key(v)) << 32) | static_cast<uint32_t>(row);
-        atomicMax(&best[b], cand);
-      }
-    }
-  }
-  if constexpr (AMAX) {
-    __syncthreads();
-    if (threadIdx.x < batch)
-      atomicMax(&amax[threadIdx.x * kArgmaxSlots + (blockIdx.x & (kArgmaxSlots - 1))], best[threadIdx.x]);
-  }
-}
-
-template <int NT>
-size_t rows64_smem() {
-  const size_t dig = 2 * static_cast<size_t>(Rows64<NT>::kN) * Rows64<NT>::kPitch;
-  const size_t cs = 64 * static_cast<size_t>(Rows64<NT>::kN) * 4;
-  return dig > cs ? dig : cs;
-}
-
-template <int NT, int EPI, bool AMAX>
-void go_rows64(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, const float* pow2, float* O,
-               int64_t osb, int64_t osr, int rows, int batch, int chunks, unsigned long long* amax, hipStream_t st) {
-  const size_t smem = rows64_smem<NT>();
-  static bool raised = false;
-  if (!raised && smem > 65536) {
-    PIA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_rows64<NT, EPI, AMAX>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
-    raised = true;
-  }
-  hipLaunchKernelGGL((k_gemm_rows64<NT, EPI, AMAX>), dim3((rows + 63) / 64, chunks), dim3(kThreads), smem, st, W, ldw,
-                     S, D, kpad, pow2, O, osb, osr, rows, batch, amax);
-}
-
-template <int NT>
-void go_dec(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, const float* pow2, float* O,
-            int64_t osb, int64_t osr, int rows, int batch, int chunks, Epi epi, unsigned long long* amax,
-            const DecSplitWork* split, hipStream_t st) {
-  // Tall matrices: 64-row tiles with the digits shared through LDS (enough tiles to fill the
-  // CUs); short ones: 16-row tiles whose 4 wavefronts split K.
-  if (static_cast<int64_t>((rows + 63) / 64) * chunks >= 96) {
-    if (epi == Epi::Add) go_rows64<NT, kEpiAdd, false>(W, ldw, S, D, kpad, pow2, O, osb, osr, rows, batch, chunks, amax, st);
-    else if (epi == Epi::Swiglu)
-      go_rows64<NT, kEpiSwiglu, false>(W, ldw, S, D, kpad, pow2, O, osb, osr, rows, batch, chunks, amax, st);
-    else if (amax) go_rows64<NT, kEpiStore, true>(W, ldw, S, D, kpad, pow2, O, osb, osr, rows, batch, chunks, amax, st);
-    else go_rows64<NT, kEpiStore, false>(W, ldw, S, D, kpad, pow2, O, osb, osr, rows, batch, chunks, amax, st);
-    return;
-  }
-  // Split K so that a launch has about kDecTargetGroups workgroups, each slice at least
-  // kDecMinSteps k-steps long.
-  const int64_t tiles = static_cast<int64_t>((rows + 15) / 16) * chunks;
+DecPlan plan_dec(int64_t rows, int64_t kpad, int nb, int64_t chunks, bool split_ok) {
+  const int ng = (nb + 15) / 16;
+  // Two row tiles per wave halve the digit operand's traffic per weight byte (L2 -> LDS ->
+  // registers), which is what limits these launches from 32 entries on; they pay where the
+  // matrix still fills the CUs with 128-row tiles (measured: Llama-3-8B gate/up yes; q/k/v, o,
+  // down and every TinyLlama projection no).
+  int rt = ng >= 2 && rows >= 24576 ? 2 : 1;
+  if (const char* e = std::getenv("PIA_DEC_RT")) rt = std::atoi(e) == 1 ? 1 : 2;
+  const int64_t tiles = (rows + 64 * rt - 1) / (64 * rt) * chunks;
   int nsplit = 1;
-  // Below three digit tiles (batch < 11) a workgroup's MFMA work per k-step is too small for
-  // the slice handshake to pay off.
-  if (split && split->ws && NT >= kDecMinSplitTiles && tiles <= split->max_tiles) {
-    const int64_t want = (kDecTargetGroups + tiles - 1) / tiles;
+  if (split_ok) {
+    int64_t target = kDecTargetGroups;
+    if (const char* e = std::getenv("PIA_DEC_TARGET")) target = std::max<int64_t>(1, std::atoll(e));
+    // Split only launches that leave most CUs idle: the slices' partial sums cost a round trip
+    // through the coherence point (two workgroups fit on a CU).
+    const int64_t want = 2 * tiles <= target ? (target + tiles - 1) / tiles : 1;
     const int64_t cap = (kpad / 64) / kDecMinSteps;
     nsplit = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({want, cap, kDecMaxSplit})));
+    if (tiles * nsplit > kDecSplitPairs) nsplit = static_cast<int>(std::max<int64_t>(1, kDecSplitPairs / tiles));
   }
+  return {rt, nsplit};
+}
+
+template <int NG, int RT, int PD>
+void go_dec_rt(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, int nrows, const float* pow2, float* O,
+               int64_t osb, int64_t osr, int rows, int batch, int chunks, Epi epi, unsigned long long* amax,
+               int nsplit, const DecSplitWork* split, hipStream_t st) {
   unsigned long long* ws = nsplit > 1 ? split->ws : nullptr;
   unsigned* cnt = nsplit > 1 ? split->cnt : nullptr;
-  dim3 grid((rows + 15) / 16, chunks, nsplit);
-  if (epi == Epi::Add)
-    hipLaunchKernelGGL((k_gemm_dec<NT, kEpiAdd, false>), grid, dim3(kThreads), 0, st, W, ldw, S, D, kpad, pow2, O, osb,
-                       osr, rows, batch, amax, ws, cnt);
-  else if (epi == Epi::Swiglu)
-    hipLaunchKernelGGL((k_gemm_dec<NT, kEpiSwiglu, false>), grid, dim3(kThreads), 0, st, W, ldw, S, D, kpad, pow2, O,
-                       osb, osr, rows, batch, amax, ws, cnt);
-  else if (amax)
-    hipLaunchKernelGGL((k_gemm_dec<NT, kEpiStore, true>), grid, dim3(kThreads), 0, st, W, ldw, S, D, kpad, pow2, O,
-                       osb, osr, rows, batch, amax, ws, cnt);
-  else
-    hipLaunchKernelGGL((k_gemm_dec<NT, kEpiStore, false>), grid, dim3(kThreads), 0, st, W, ldw, S, D, kpad, pow2, O,
-                       osb, osr, rows, batch, amax, ws, cnt);
+  const dim3 grid((rows + 64 * RT - 1) / (64 * RT), chunks, nsplit);
+#define PIA_DEC(E, A)                                                                                          \
+  hipLaunchKernelGGL((k_gemm_dec<NG, RT, PD, E, A>), grid, dim3(kThreads), 0, st, W, ldw, S, D, kpad, nrows, pow2, O, osb, \
+                     osr, rows, batch, amax, ws, cnt)
+  if (epi == Epi::Add) PIA_DEC(kEpiAdd, false);
+  else if (epi == Epi::Swiglu) PIA_DEC(kEpiSwiglu, false);
+  else if (amax) PIA_DEC(kEpiStore, true);
+  else PIA_DEC(kEpiStore, false);
+#undef PIA_DEC
+}
+
+template <int NG>
+void go_dec(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, int nrows, const float* pow2, float* O,
+            int64_t osb, int64_t osr, int rows, int batch, int chunks, Epi epi, unsigned long long* amax,
+            const DecSplitWork* split, hipStream_t st) {
+  const DecPlan pl = plan_dec(rows, kpad, batch, chunks, split && split->ws);
+  // Ring depth: k-steps in flight per wave (register budget: acc RT*3*NG*4, ring PD*(RT + DV)*4).
+  // Ring depth 4: two workgroups per CU (registers <= 256 per lane, no accumulator copies)
+  // beat a deeper ring at one workgroup per CU on every measured shape.
+  constexpr int PD = 4;
+  if (pl.rt == 2) go_dec_rt<NG, 2, PD>(W, ldw, S, D, kpad, nrows, pow2, O, osb, osr, rows, batch, chunks, epi, amax, pl.nsplit, split, st);
+  else go_dec_rt<NG, 1, PD>(W, ldw, S, D, kpad, nrows, pow2, O, osb, osr, rows, batch, chunks, epi, amax, pl.nsplit, split, st);
 }
 
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -598,7 +599,7 @@ constexpr size_t kSmem = 2 * kStage > 64 * kBN * 4 ? 2 * kStage : 64 * kBN * 4;
 template <int EPI>
 __global__ __launch_bounds__(kThreads) void k_gemm_tile(const int8_t* __restrict__ W, int64_t ldw,
                                                         const float* __restrict__ S, const int8_t* __restrict__ D,
-                                                        int kpad, const float* __restrict__ pow2,
+                                                        int kpad, int nrows, const float* __restrict__ pow2,
                                                         float* __restrict__ O, int64_t osb, int64_t osr, int rows) {
   using namespace tile;
   extern __shared__ __align__(16) int8_t lds[];
@@ -617,14 +618,15 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const int8_t* __restrict
   for (int u = 0; u < kWLoads; ++u)
     wsrc[u] = W + static_cast<int64_t>(min(row0 + trow + 64 * u, rows - 1)) * ldw + seg * 16;
 #pragma unroll
-  for (int u = 0; u < kDLoads; ++u) dsrc[u] = D + static_cast<int64_t>(col0 + trow + 64 * u) * kpad + seg * 16;
+  for (int u = 0; u < kDLoads; ++u) dsrc[u] = D + static_cast<int64_t>(col0 + trow + 64 * u) * 64 + seg * 16;
   v4i wreg[kWLoads], dreg[kDLoads];
   auto gload = [&](int kt) {
     const int64_t off = static_cast<int64_t>(kt) * kBK;
+    const int64_t doff = static_cast<int64_t>(kt) * nrows * 64;  // k-step-major digits
 #pragma unroll
     for (int u = 0; u < kWLoads; ++u) wreg[u] = *reinterpret_cast<const v4i*>(wsrc[u] + off);
 #pragma unroll
-    for (int u = 0; u < kDLoads; ++u) dreg[u] = *reinterpret_cast<const v4i*>(dsrc[u] + off);
+    for (int u = 0; u < kDLoads; ++u) dreg[u] = *reinterpret_cast<const v4i*>(dsrc[u] + doff);
   };
   auto sstore = [&](int buf) {
     int8_t* ws = lds + buf * kStage;
@@ -693,13 +695,13 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const int8_t* __restrict
     for (int idx = tid; idx < 64 * (kBN / 3); idx += kThreads) {
       const int r = idx / (kBN / 3), b = idx % (kBN / 3);
       const int row = row0 + half * 64 + r;
-      const int* cr = ct + r * kBN + 3 * b;
-      const int64_t sum = static_cast<int64_t>(cr[0]) + 256 * static_cast<int64_t>(cr[1]) + 65536 * static_cast<int64_t>(cr[2]);
+      const int* cr = ct + r * kBN + digit_row(b, 0);  // digits j at cr[16 j]
+      const int64_t sum = static_cast<int64_t>(cr[0]) + 256 * static_cast<int64_t>(cr[16]) + 65536 * static_cast<int64_t>(cr[32]);
       const float y = static_cast<float>(sum) * pow2[b0 + b];
       if constexpr (EPI == kEpiSwiglu) {
         if ((r & 1) == 0 && row + 1 < rows) {
           const int* cu = cr + kBN;
-          const int64_t su = static_cast<int64_t>(cu[0]) + 256 * static_cast<int64_t>(cu[1]) + 65536 * static_cast<int64_t>(cu[2]);
+          const int64_t su = static_cast<int64_t>(cu[0]) + 256 * static_cast<int64_t>(cu[16]) + 65536 * static_cast<int64_t>(cu[32]);
           const float yu = static_cast<float>(su) * pow2[b0 + b];
           const float g = y * S[row];
           const float u = yu * S[row + 1];
@@ -718,8 +720,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const int8_t* __restrict
 }
 
 template <int EPI>
-void go_tile(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, const float* pow2, float* O,
-             int64_t osb, int64_t osr, int rows, int tiles_n, hipStream_t st) {
+void go_tile(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, int nrows, const float* pow2,
+             float* O, int64_t osb, int64_t osr, int rows, int tiles_n, hipStream_t st) {
   static bool raised = false;
   if (!raised && tile::kSmem > 65536) {
     PIA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_tile<EPI>),
@@ -727,29 +729,27 @@ void go_tile(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int 
     raised = true;
   }
   hipLaunchKernelGGL((k_gemm_tile<EPI>), dim3((rows + tile::kBM - 1) / tile::kBM, tiles_n), dim3(kThreads), tile::kSmem,
-                     st, W, ldw, S, D, kpad, pow2, O, osb, osr, rows);
+                     st, W, ldw, S, D, kpad, nrows, pow2, O, osb, osr, rows);
 }
 
 }  // namespace
 
-int64_t digit_cols(int64_t batch) { return (3 * batch + 15) / 16 * 16; }
-
-// Digit rows written by k_xdigits: whole triples covering digit_cols(batch) columns.
-int64_t digit_rows(int64_t batch) { return (digit_cols(batch) + 2) / 3 * 3; }
+// Groups of 16 batch entries: 48 digit rows and 16 power-of-two factors each.
+int64_t digit_groups(int64_t batch) { return (batch + 15) / 16; }
 
 int64_t xdigits_bytes(int64_t batch, int64_t cols) {
-  const int64_t kpad = (cols + 63) / 64 * 64;
-  return (digit_rows(batch) * kpad + 255) / 256 * 256 + digit_rows(batch) / 3 * 4;
+  const int64_t kpad = (cols + 63) / 64 * 64, g = digit_groups(batch);
+  return (48 * g * kpad + 255) / 256 * 256 + 16 * g * 4;
 }
 
 void launch_xdigits(const float* x, int64_t ldx, const float* norm_w, float eps, int64_t batch, int64_t cols,
                     void* xq, hipStream_t st) {
   PIA_REQUIRE(batch > 0 && cols > 0 && cols < (int64_t(1) << 30), "xdigits: bad shape");
   const int64_t kpad = (cols + 63) / 64 * 64;
-  const int64_t n = digit_rows(batch);
+  const int64_t n = 48 * digit_groups(batch);
   int8_t* dig = static_cast<int8_t*>(xq);
   float* pow2 = reinterpret_cast<float*>(dig + (n * kpad + 255) / 256 * 256);
-  const int64_t groups = n / 3;  // digit-column triples (batch rows, padded with zeros)
+  const int64_t groups = n / 3;  // entries written (batch rows, padded with zero rows to whole groups)
   const bool vec = cols % 4 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
                    (!norm_w || (reinterpret_cast<uintptr_t>(norm_w) & 15) == 0);
   const int64_t v4 = (cols / 4 + 63) / 64;  // float4 per lane
@@ -759,7 +759,7 @@ void launch_xdigits(const float* x, int64_t ldx, const float* norm_w, float eps,
 #define PIA_XDW(V, W)                                                                                            \
   hipLaunchKernelGGL((k_xdigits_wave<V, W>), dim3(static_cast<unsigned>((groups + 4 / W - 1) / (4 / W))), dim3(256), \
                      0, st, x, ldx, norm_w, eps, static_cast<int>(cols), static_cast<int>(batch),                 \
-                     static_cast<int>(groups), static_cast<int>(kpad), dig, pow2)
+                     static_cast<int>(groups), static_cast<int>(kpad), static_cast<int>(n), dig, pow2)
     if (v4 <= 8) PIA_XDW(8, 1);
     else if (v4 <= 16) PIA_XDW(8, 2);
     else if (v4 <= 32) PIA_XDW(8, 4);
@@ -767,12 +767,18 @@ void launch_xdigits(const float* x, int64_t ldx, const float* norm_w, float eps,
 #undef PIA_XDW
   } else {
     hipLaunchKernelGGL(k_xdigits, dim3(static_cast<unsigned>(groups)), dim3(kThreads), 0, st, x, ldx, norm_w, eps,
-                       static_cast<int>(cols), static_cast<int>(batch), static_cast<int>(kpad), dig, pow2);
+                       static_cast<int>(cols), static_cast<int>(batch), static_cast<int>(kpad), static_cast<int>(n), dig,
+                       pow2);
   }
   PIA_HIP(hipGetLastError());
 }
 
-int64_t dec_split_bytes(int64_t max_tiles) { return max_tiles * kDecMaxSplit * 16 * 64 * 8 + max_tiles * 4; }
+int64_t dec_split_bytes() { return kDecSplitPairs * 128 * 64 * 8 + kDecSplitPairs * 4; }
+
+DecSplitWork dec_split_work(void* base) {
+  return DecSplitWork{static_cast<unsigned long long*>(base),
+                      reinterpret_cast<unsigned*>(static_cast<char*>(base) + kDecSplitPairs * 128 * 64 * 8)};
+}
 
 void launch_gemm_i8_mfma(const int8_t* W, int64_t ldw, const float* scales, const void* xq, float* out, int64_t osb,
                          int64_t osr, int64_t rows, int64_t cols, int64_t batch, Epi epi, unsigned long long* amax,
@@ -784,34 +790,30 @@ void launch_gemm_i8_mfma(const int8_t* W, int64_t ldw, const float* scales, cons
   PIA_REQUIRE(epi != Epi::Swiglu || rows % 2 == 0, "gemm: SwiGLU needs interleaved row pairs");
   PIA_REQUIRE(!amax || epi == Epi::Store, "gemm: fused argmax needs the Store epilogue");
   const int8_t* dig = static_cast<const int8_t*>(xq);
-  const int64_t n = digit_rows(batch);
+  const int64_t n = 48 * digit_groups(batch);
   const float* pow2 = reinterpret_cast<const float*>(dig + (n * kpad + 255) / 256 * 256);
-  const int r = static_cast<int>(rows), k = static_cast<int>(kpad);
-  // Column tiles of 64 batch entries (12 x 16 digit columns) along grid.y, then the ragged
+  const int r = static_cast<int>(rows), k = static_cast<int>(kpad), nr = static_cast<int>(n);
+  // Chunks of 64 batch entries (4 groups, 192 digit rows) along grid.y, then the ragged
   // remainder as its own launch.
   const int64_t full = batch / 64;
   auto launch = [&](int64_t b0, int64_t chunks, int nb) {
-    const int nt = static_cast<int>(digit_cols(nb) / 16);
-    const int8_t* D = dig + 3 * b0 * kpad;
+    const int8_t* D = dig + 3 * b0 * 64;  // b0 is a multiple of 64: whole groups (rows 3 b0 ..)
     float* O = out + b0 * osb;
     unsigned long long* am = amax ? amax + b0 * kArgmaxSlots : nullptr;
     const float* p2 = pow2 + b0;
-    switch (nt) {
-#define PIA_NT(N)                                                                                     \
-  case N:                                                                                             \
-    go_dec<N>(W, ldw, scales, D, k, p2, O, osb, osr, r, nb, static_cast<int>(chunks), epi, am, split, st); \
-    break;
-      PIA_NT(1) PIA_NT(2) PIA_NT(3) PIA_NT(4) PIA_NT(5) PIA_NT(6) PIA_NT(7) PIA_NT(8) PIA_NT(9) PIA_NT(10)
-      PIA_NT(11) PIA_NT(12)
-#undef PIA_NT
-      default: fail(PIA_ERR_INVALID, "gemm: bad column tile");
+    const int c = static_cast<int>(chunks);
+    switch (digit_groups(nb)) {
+      case 1: go_dec<1>(W, ldw, scales, D, k, nr, p2, O, osb, osr, r, nb, c, epi, am, split, st); break;
+      case 2: go_dec<2>(W, ldw, scales, D, k, nr, p2, O, osb, osr, r, nb, c, epi, am, split, st); break;
+      case 3: go_dec<3>(W, ldw, scales, D, k, nr, p2, O, osb, osr, r, nb, c, epi, am, split, st); break;
+      default: go_dec<4>(W, ldw, scales, D, k, nr, p2, O, osb, osr, r, nb, c, epi, am, split, st); break;
     }
   };
   if (full >= kTileMinChunks && !amax) {
     // Many batch entries (prefill): the LDS-tiled kernel over the whole 64-entry chunks.
-    if (epi == Epi::Add) go_tile<kEpiAdd>(W, ldw, scales, dig, k, pow2, out, osb, osr, r, static_cast<int>(full), st);
-    else if (epi == Epi::Swiglu) go_tile<kEpiSwiglu>(W, ldw, scales, dig, k, pow2, out, osb, osr, r, static_cast<int>(full), st);
-    else go_tile<kEpiStore>(W, ldw, scales, dig, k, pow2, out, osb, osr, r, static_cast<int>(full), st);
+    if (epi == Epi::Add) go_tile<kEpiAdd>(W, ldw, scales, dig, k, nr, pow2, out, osb, osr, r, static_cast<int>(full), st);
+    else if (epi == Epi::Swiglu) go_tile<kEpiSwiglu>(W, ldw, scales, dig, k, nr, pow2, out, osb, osr, r, static_cast<int>(full), st);
+    else go_tile<kEpiStore>(W, ldw, scales, dig, k, nr, pow2, out, osb, osr, r, static_cast<int>(full), st);
   } else if (full) {
     launch(0, full, 64);
   }
