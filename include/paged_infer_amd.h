@@ -98,6 +98,15 @@ pia_status pia_qlinear_apply_dev(pia_context* ctx, float* out_br, const float* x
 /* Host-pointer form of the above (same reference function), synchronous. */
 pia_status pia_qlinear_apply(pia_context* ctx, float* out_br, const float* x_br, const int8_t* w,
                              const float* scales, int64_t batch, int64_t rows, int64_t cols);
+/* No counterpart in the reference: pia_qlinear_apply_dev for callers that cannot allocate
+ * device memory (graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * kernels and results; the matrix-core path's scratch (activation digits, split-K partials) is a
+ * fixed per-device array set up when a context is created, so it allocates nothing. Limits:
+ * batch <= 64, cols <= 16384 (PIA_ERR_INVALID beyond). Calls on one GPU share that scratch:
+ * overlapping calls on one device race (order them on one stream). */
+pia_status pia_qlinear_apply_noalloc_dev(pia_context* ctx, float* out_br, const float* x_br, const int8_t* w,
+                                         const float* scales, int64_t batch, int64_t rows, int64_t cols,
+                                         void* stream);
 
 /* KV cache layout (src/memory/layout.rs:17-78): f32
  * [num_layers][num_blocks][block_size][num_kv_heads][k|v][head_dim]. */

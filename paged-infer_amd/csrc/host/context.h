@@ -71,6 +71,12 @@ void sample_with_context(pia_context* ctx, int32_t* out, const float* logits, in
 // kMfmaMinBatch rows whose rows are whole 64-byte k-steps run the matrix-core path (digits in
 // the context's workspace, so calls on one context must be ordered), the rest the GEMV.
 void launch_projection(pia_context* ctx, const GemvArgs& g, hipStream_t st);
+// Whether launch_projection takes the matrix-core path for g.
+bool projection_on_matrix_cores(const GemvArgs& g);
+// The allocation-free projection's per-device scratch (projection_noalloc.hip): set up once
+// per device when a context is created on it.
+void noalloc_setup(int device, hipStream_t st);
+int64_t noalloc_scratch_bytes();
 void model_set_proj_bf16_dev(pia_model* m, int64_t layer, int32_t which, int kind, const uint16_t* src, int64_t rows,
                              int64_t cols);
 }  // namespace pia

@@ -145,10 +145,14 @@ void sample_with_context(pia_context* ctx, int32_t* out, const float* logits, in
   }
   launch_sample(logits, ld, n, vocab, params, rng_state, out, mode, ctx->sample_ws.ptr, ctx->sample_ws.bytes, st);
 }
-void launch_projection(pia_context* ctx, const GemvArgs& g, hipStream_t st) {
+bool projection_on_matrix_cores(const GemvArgs& g) {
   const bool a16 = (reinterpret_cast<uintptr_t>(g.W) & 15) == 0 && (reinterpret_cast<uintptr_t>(g.x) & 15) == 0;
-  if (!(g.wkind == 1 && g.batch >= kMfmaMinBatch && g.cols % 64 == 0 && g.ldw % 64 == 0 && g.ldx % 4 == 0 && a16 &&
-        g.norm_w == nullptr && g.amax == nullptr && g.scales != nullptr)) {
+  return g.wkind == 1 && g.batch >= kMfmaMinBatch && g.cols % 64 == 0 && g.ldw % 64 == 0 && g.ldx % 4 == 0 && a16 &&
+         g.norm_w == nullptr && g.amax == nullptr && g.scales != nullptr;
+}
+
+void launch_projection(pia_context* ctx, const GemvArgs& g, hipStream_t st) {
+  if (!projection_on_matrix_cores(g)) {
     launch_gemv(g, st);
     return;
   }
@@ -191,6 +195,13 @@ pia_status pia_context_create(int device, pia_context** out) {
   ctx->device = device;
   ctx->num_cus = prop.multiProcessorCount;
   PIA_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+  try {
+    noalloc_setup(device, ctx->stream);
+  } catch (...) {
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    throw;
+  }
   *out = ctx;
   PIA_API_END
 }

@@ -55,16 +55,17 @@ void launch_gemv(const GemvArgs& args, hipStream_t st);
 int64_t xdigits_bytes(int64_t batch, int64_t cols);
 void launch_xdigits(const float* x, int64_t ldx, const float* norm_w, float eps, int64_t batch, int64_t cols,
                     void* xq, hipStream_t st);
-// Split-K workspace of the decode GEMM: exact 64-bit partial sums of up to kDecSplitPairs
-// (row tile, K slice) pairs of 128 rows x 64 entries, then one counter per row tile (zero when
-// allocated, left zero by every launch). Launches that would need more pairs split less.
+// Split-K workspace of the decode GEMM: exact 64-bit partial sums of up to `pairs` (row tile,
+// K slice) pairs of 128 rows x 64 entries, then one counter per row tile (zero when allocated,
+// left zero by every launch). Launches that would need more pairs split less.
 constexpr int64_t kDecSplitPairs = 512;
 struct DecSplitWork {
   unsigned long long* ws;
   unsigned* cnt;
+  int64_t pairs;
 };
-int64_t dec_split_bytes();
-DecSplitWork dec_split_work(void* base);
+int64_t dec_split_bytes(int64_t pairs = kDecSplitPairs);
+DecSplitWork dec_split_work(void* base, int64_t pairs = kDecSplitPairs);
 void launch_gemm_i8_mfma(const int8_t* W, int64_t ldw, const float* scales, const void* xq, float* out, int64_t osb,
                          int64_t osr, int64_t rows, int64_t cols, int64_t batch, Epi epi, unsigned long long* amax,
                          const DecSplitWork* split, hipStream_t st);

@@ -528,7 +528,8 @@ struct DecPlan {
   int rt, nsplit;
 };
 
-DecPlan plan_dec(int64_t rows, int64_t kpad, int nb, int64_t chunks, bool split_ok) {
+DecPlan plan_dec(int64_t rows, int64_t kpad, int nb, int64_t chunks, int64_t max_pairs) {
+  const bool split_ok = max_pairs > 1;
   const int ng = (nb + 15) / 16;
   // Two row tiles per wave halve the digit operand's traffic per weight byte (L2 -> LDS ->
   // registers), which is what limits these launches from 32 entries on; they pay where the
@@ -546,7 +547,7 @@ DecPlan plan_dec(int64_t rows, int64_t kpad, int nb, int64_t chunks, bool split_
     const int64_t want = 2 * tiles <= target ? (target + tiles - 1) / tiles : 1;
     const int64_t cap = (kpad / 64) / kDecMinSteps;
     nsplit = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({want, cap, kDecMaxSplit})));
-    if (tiles * nsplit > kDecSplitPairs) nsplit = static_cast<int>(std::max<int64_t>(1, kDecSplitPairs / tiles));
+    if (tiles * nsplit > max_pairs) nsplit = static_cast<int>(std::max<int64_t>(1, max_pairs / tiles));
   }
   return {rt, nsplit};
 }
@@ -572,7 +573,7 @@ template <int NG>
 void go_dec(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, int nrows, const float* pow2, float* O,
             int64_t osb, int64_t osr, int rows, int batch, int chunks, Epi epi, unsigned long long* amax,
             const DecSplitWork* split, hipStream_t st) {
-  const DecPlan pl = plan_dec(rows, kpad, batch, chunks, split && split->ws);
+  const DecPlan pl = plan_dec(rows, kpad, batch, chunks, split && split->ws ? split->pairs : 0);
   // Ring depth: k-steps in flight per wave (register budget: acc RT*3*NG*4, ring PD*(RT + DV)*4).
   // Ring depth 4: two workgroups per CU (registers <= 256 per lane, no accumulator copies)
   // beat a deeper ring at one workgroup per CU on every measured shape.
@@ -773,11 +774,11 @@ void launch_xdigits(const float* x, int64_t ldx, const float* norm_w, float eps,
   PIA_HIP(hipGetLastError());
 }
 
-int64_t dec_split_bytes() { return kDecSplitPairs * 128 * 64 * 8 + kDecSplitPairs * 4; }
+int64_t dec_split_bytes(int64_t pairs) { return pairs * 128 * 64 * 8 + pairs * 4; }
 
-DecSplitWork dec_split_work(void* base) {
+DecSplitWork dec_split_work(void* base, int64_t pairs) {
   return DecSplitWork{static_cast<unsigned long long*>(base),
-                      reinterpret_cast<unsigned*>(static_cast<char*>(base) + kDecSplitPairs * 128 * 64 * 8)};
+                      reinterpret_cast<unsigned*>(static_cast<char*>(base) + pairs * 128 * 64 * 8), pairs};
 }
 
 void launch_gemm_i8_mfma(const int8_t* W, int64_t ldw, const float* scales, const void* xq, float* out, int64_t osb,

@@ -107,6 +107,7 @@ _SIGS = {
     "pia_matmat_i8": (I32, [P, P, P, P, P, I64, I64, I64]),
     "pia_matmat_i8_dev": (I32, [P, P, P, P, P, I64, I64, I64, P]),
     "pia_qlinear_apply_dev": (I32, [P, P, P, P, P, I64, I64, I64, P]),
+    "pia_qlinear_apply_noalloc_dev": (I32, [P, P, P, P, P, I64, I64, I64, P]),
     "pia_qlinear_apply": (I32, [P, P, P, P, P, I64, I64, I64]),
     "pia_paged_attention_dev": (I32, [P, P, P, P, C.POINTER(KvLayout), I64, P, P, I64, I64, P]),
     "pia_kv_write_dev": (I32, [P, P, C.POINTER(KvLayout), P, P, P, P, I64, I64, P]),
