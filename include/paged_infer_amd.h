@@ -275,6 +275,13 @@ pia_status pia_model_prefill(pia_model* m, const uint32_t* tokens, int64_t n, in
  * 1 persistent, -1 none yet). No counterpart in the reference (it has no GPU int8 path). */
 pia_status pia_model_set_decode_path(pia_model* m, int32_t path);
 int32_t pia_model_decode_path_used(const pia_model* m);
+/* Diagnostics (no counterpart in the reference): what the last pia_model_decode copied from the
+ * host. Block tables stay on the device between decode steps (per-entry slots); a step sends
+ * its tokens and entries, plus only the table slots whose block ids changed since the previous
+ * step (append_block, copy-on-write remap) as (slot, id) pairs, or the whole table image when the
+ * batch's layout changed or most slots differ. *bytes = host-to-device bytes of the step,
+ * *table_patches = slots patched, *table_full = 1 when the image was re-sent. */
+pia_status pia_model_last_upload(const pia_model* m, int64_t* bytes, int64_t* table_patches, int32_t* table_full);
 
 /* ------------------------------------------------------------------------------------ */
 /* Sampling (src/sampling.rs).                                                            */

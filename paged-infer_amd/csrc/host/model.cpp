@@ -100,6 +100,16 @@ struct pia_model {
   bool replay_graphs = true;  // diagnostic PIA_NO_GRAPH=1: decode steps launch eagerly
   int64_t logit_rows = 0;  // rows of `logits` the last decode / prefill wrote
   DeviceBuffer samp;       // sampling parameters, generator states and drawn tokens
+  // Decode block tables, device-resident between steps: entry b's table in slots
+  // [b * tab_cap, b * tab_cap + table_len). tab_mirror holds what the device holds (-1: unknown),
+  // so a step uploads only the slots that changed (append_block / copy-on-write remap).
+  DeviceBuffer tab_dev;
+  std::vector<int32_t> tab_mirror;
+  int64_t tab_cap = 0, tab_rows = 0;
+  // The last decode's host-to-device bytes: step inputs, table patches, whether the whole
+  // table image was re-sent.
+  int64_t up_bytes = 0, up_patches = 0;
+  bool up_full = false;
   PinnedBuffer pin, pin_out;
   Prof prof;
 
@@ -720,6 +730,15 @@ pia_status pia_model_set_decode_path(pia_model* m, int32_t path) {
 
 int32_t pia_model_decode_path_used(const pia_model* m) { return m ? m->last_path : -1; }
 
+pia_status pia_model_last_upload(const pia_model* m, int64_t* bytes, int64_t* table_patches, int32_t* table_full) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(m, "null model");
+  if (bytes) *bytes = m->up_bytes;
+  if (table_patches) *table_patches = m->up_patches;
+  if (table_full) *table_full = m->up_full ? 1 : 0;
+  PIA_API_END
+}
+
 pia_status pia_model_profile(pia_model* m, int32_t enable) {
   PIA_API_BEGIN
   PIA_REQUIRE(m, "null model");
@@ -839,6 +858,78 @@ pia_model::StepDev upload_step(pia_model* m, const std::vector<int32_t>& tok, co
           reinterpret_cast<const int32_t*>(d + off_t)};
 }
 
+// Decode step inputs: tokens and entries (every step) plus the block tables, which stay on the
+// device in per-entry slots of tab_cap ids; only the slots whose ids differ from the device copy
+// travel, as (slot, id) pairs applied by a scatter kernel, unless the layout changed or most
+// slots differ (then the whole image). Host entries index the caller's flat `tables`; the
+// device entries index the resident slots.
+pia_model::StepDev upload_decode_step(pia_model* m, const std::vector<int32_t>& tok,
+                                      const std::vector<pia_attn_entry>& ent, const int32_t* tables) {
+  const int64_t n = static_cast<int64_t>(tok.size());
+  int64_t maxlen = 1;
+  for (const auto& e : ent) maxlen = std::max<int64_t>(maxlen, e.table_len);
+  const int64_t cap = round_up(maxlen, 64);
+  bool full = false;
+  if (cap > m->tab_cap || n > m->tab_rows) {
+    const int64_t ncap = std::max(cap, m->tab_cap), nrows = std::max<int64_t>(round_up(n, 8), m->tab_rows);
+    PIA_HIP(hipStreamSynchronize(m->st()));
+    m->drop_graphs();  // captured steps hold the old table address
+    m->tab_dev.release();
+    m->tab_dev.ensure(nrows * ncap * 4);
+    m->tab_cap = ncap, m->tab_rows = nrows;
+    m->tab_mirror.assign(nrows * ncap, -1);
+    full = true;
+  }
+  const int64_t tc = m->tab_cap;
+  std::vector<int32_t> patch;
+  if (!full) {
+    for (int64_t b = 0; b < n; ++b)
+      for (int32_t i = 0; i < ent[b].table_len; ++i) {
+        const int64_t slot = b * tc + i;
+        const int32_t id = tables[ent[b].table_off + i];
+        if (m->tab_mirror[slot] != id) {
+          patch.push_back(static_cast<int32_t>(slot));
+          patch.push_back(id);
+        }
+      }
+    full = static_cast<int64_t>(patch.size() / 2) * 8 > n * tc;  // most slots changed: send the image
+  }
+  std::vector<pia_attn_entry> dent(ent);
+  for (int64_t b = 0; b < n; ++b) dent[b].table_off = static_cast<int32_t>(b * tc);
+  const size_t off_e = round_up(n * 4, 256), off_t = off_e + round_up(n * sizeof(pia_attn_entry), 256);
+  const size_t tab_bytes = full ? static_cast<size_t>(n * tc * 4) : patch.size() * 4;
+  const size_t total = off_t + round_up(std::max<size_t>(tab_bytes, 4), 256);
+  PIA_HIP(hipStreamSynchronize(m->st()));  // the pinned staging buffer may still be in flight
+  m->pin.ensure(total);
+  m->grow(m->step, std::max<size_t>(total, 1 << 16));
+  char* p = static_cast<char*>(m->pin.ptr);
+  std::memcpy(p, tok.data(), n * 4);
+  std::memcpy(p + off_e, dent.data(), n * sizeof(pia_attn_entry));
+  char* d = static_cast<char*>(m->step.ptr);
+  if (full) {
+    auto* img = reinterpret_cast<int32_t*>(p + off_t);
+    for (int64_t b = 0; b < n; ++b)
+      for (int64_t i = 0; i < tc; ++i) {
+        const int32_t id = i < ent[b].table_len ? tables[ent[b].table_off + i] : 0;
+        img[b * tc + i] = id;
+        m->tab_mirror[b * tc + i] = id;
+      }
+    PIA_HIP(hipMemcpyAsync(d, p, off_t, hipMemcpyHostToDevice, m->st()));
+    PIA_HIP(hipMemcpyAsync(m->tab_dev.ptr, img, tab_bytes, hipMemcpyHostToDevice, m->st()));
+  } else {
+    if (!patch.empty()) std::memcpy(p + off_t, patch.data(), tab_bytes);
+    PIA_HIP(hipMemcpyAsync(d, p, off_t + tab_bytes, hipMemcpyHostToDevice, m->st()));
+    launch_table_patch(m->tab_dev.as<int32_t>(), reinterpret_cast<const int32_t*>(d + off_t),
+                       static_cast<int64_t>(patch.size() / 2), m->st());
+    for (size_t i = 0; i < patch.size(); i += 2) m->tab_mirror[patch[i]] = patch[i + 1];
+  }
+  m->up_bytes = static_cast<int64_t>(n * 4 + n * sizeof(pia_attn_entry) + tab_bytes);
+  m->up_patches = static_cast<int64_t>(patch.size() / 2);
+  m->up_full = full;
+  return {reinterpret_cast<const int32_t*>(d), reinterpret_cast<const pia_attn_entry*>(d + off_e),
+          m->tab_dev.as<int32_t>()};
+}
+
 int64_t mapped_in_window(const pia_attn_entry& e, int64_t bs) {
   // Tokens of start..=pos that fall inside mapped logical blocks (the K/V actually read).
   const int64_t end = std::min<int64_t>(e.pos + 1, static_cast<int64_t>(e.table_len) * bs);
@@ -909,7 +1000,7 @@ pia_status pia_model_decode(pia_model* m, const uint32_t* tokens, const int64_t*
   if (wb) m->grow(m->attn_work, wb);
   const bool step = batch == 1 && m->step_ready() &&
                     max_window <= m->step_shape.max_splits * m->step_shape.max_tokens;
-  const pia_model::StepDev in = upload_step(m, tok, ent, tables, ntab);
+  const pia_model::StepDev in = upload_decode_step(m, tok, ent, tables);
   if (step) {
     m->run_step({2, 1, 0, 0, 0, 0}, true, [&] {
       m->timed(7, m->step_bytes(mapped), [&] { m->launch_step(in); });

@@ -217,4 +217,7 @@ void launch_decode_step(const StepParams& p, const StepShape& s, int num_cus, hi
 
 void launch_copy_block(float* kv, const pia_kv_layout& layout, int64_t src, int64_t dst, hipStream_t st);
 
+// tab[patch[2i]] = patch[2i + 1] for i < n (the changed slots of device-resident block tables).
+void launch_table_patch(int32_t* tab, const int32_t* patch, int64_t n, hipStream_t st);
+
 }  // namespace pia

@@ -321,6 +321,22 @@ void launch_widen_rows_bf16(const uint16_t* w, int64_t rows, int64_t cols, float
   PIA_HIP(hipGetLastError());
 }
 
+namespace {
+__global__ __launch_bounds__(kThreads) void k_table_patch(int32_t* __restrict__ tab, const int32_t* __restrict__ patch,
+                                                          int n) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) tab[patch[2 * i]] = patch[2 * i + 1];
+}
+}  // namespace
+
+void launch_table_patch(int32_t* tab, const int32_t* patch, int64_t n, hipStream_t st) {
+  PIA_REQUIRE(n >= 0 && n < (int64_t(1) << 30), "table patch: bad count");
+  if (n == 0) return;
+  hipLaunchKernelGGL(k_table_patch, dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, st,
+                     tab, patch, static_cast<int>(n));
+  PIA_HIP(hipGetLastError());
+}
+
 void launch_copy_block(float* kv, const pia_kv_layout& L, int64_t src, int64_t dst, hipStream_t st) {
   PIA_REQUIRE(src != dst, "copy_block called with src == dst");
   PIA_REQUIRE(src >= 0 && dst >= 0 && src < L.num_blocks && dst < L.num_blocks, "copy_block: block out of range");

@@ -155,6 +155,7 @@ _SIGS = {
     "pia_model_profile": (I32, [P, I32]),
     "pia_model_set_decode_path": (I32, [P, I32]),
     "pia_model_decode_path_used": (I32, [P]),
+    "pia_model_last_upload": (I32, [P, P, P, P]),
     "pia_model_profile_get": (I32, [P, P, P, P, I32]),
     "pia_model_bench_class": (I32, [P, I32, I64, I32, C.POINTER(C.c_double), C.POINTER(I64)]),
     "pia_bench_projection": (I32, [P, I64, I64, I64, I32, I32, C.POINTER(C.c_double), C.POINTER(I64)]),
@@ -665,6 +666,12 @@ class Model:
     def decode_path_used(self) -> int:
         """Path of the last decode: 0 per-kernel launches, 1 persistent step."""
         return int(lib().pia_model_decode_path_used(self.h))
+
+    def last_upload(self):
+        """(host-to-device bytes, table slots patched, whole image re-sent) of the last decode."""
+        b, pch, full = I64(), I64(), I32()
+        check(lib().pia_model_last_upload(self.h, C.byref(b), C.byref(pch), C.byref(full)))
+        return b.value, pch.value, bool(full.value)
 
     def profile_get(self):
         """(ms, algorithmic bytes, launches) per class of the last profiled call."""

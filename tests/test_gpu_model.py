@@ -437,3 +437,62 @@ def test_outlier_channels_batched_decode(ctx):
         toks_g, toks_c = am.tolist(), [orc.argmax(r) for r in lc]
         assert toks_g == toks_c
     gm.close()
+
+
+def test_device_resident_tables_patch_only_changed_slots(ctx):
+    """Block tables stay on the device between decode steps: after the first step (whole image),
+    a step sends only the slots that append_block or a copy-on-write remap changed
+    (src/memory/block_table.rs:86-93, src/engine.rs:614-693), and its host-to-device bytes are
+    exactly tokens + entries + 8 bytes per changed slot. Tokens, logits and the KV cache the steps
+    write (through the device tables) match the oracle, which reads the host tables."""
+    cfg = pia.TINY_C1
+    w = pia.synth_weights(cfg, seed=12)
+    bs, total = 16, 64
+    rng = np.random.default_rng(12)
+    gm = pia.Model(ctx, cfg, w)
+    gm.kv_alloc(total, bs)
+    om_ = orc.OracleModel(cfg, w)
+    kv = np.zeros(orc.kv_floats(cfg, total, bs), np.float32)
+    olay = om.KvLayout(cfg.layers, total, bs, cfg.kv_heads, cfg.head_dim)
+    mg, mo = pia.KvCacheManager(total, bs, prefix_cache=False), om.KvCacheManager(total, bs, prefix_cache=False)
+    seqs, tick = [], 0
+    for sid in range(4):
+        prompt = rng.integers(0, cfg.vocab, 13 + 7 * sid).tolist()
+        tick += 1
+        tg, _ = mg.admit(sid, prompt, tick)
+        ao = mo.admit(sid, prompt, tick)
+        lg, _ = gm.prefill(prompt, 0, tg.blocks())
+        lc = om_.prefill(prompt, 0, ao.table.blocks(), kv, total, bs)
+        seqs.append([sid, tg, ao.table, len(prompt), orc.argmax(lg), orc.argmax(lc)])
+    tick += 1
+    seqs.append([4, mg.fork(seqs[0][1], 4, tick), mo.fork(seqs[0][2], 4, tick)] + seqs[0][3:])
+    prev = None
+    n = len(seqs)
+    for step in range(24):
+        tick += 1
+        for s in seqs:
+            sid, tg, to, pos = s[0], s[1], s[2], s[3]
+            while len(tg) * bs <= pos:
+                assert mg.append_block(sid, tg, tick) == mo.append_block(sid, to, tick)
+            assert mg.ensure_writable(sid, tg, pos, ctx, gm.kv_ptr, gm.layout) == \
+                mo.ensure_writable(sid, to, pos, lambda a, b: olay.copy_block(kv, a, b))
+            assert tg.blocks() == to.blocks()
+        tables = [s[1].blocks() for s in seqs]
+        lg, am = gm.decode([s[4] for s in seqs], [s[3] for s in seqs], tables)
+        lc = om_.decode([s[5] for s in seqs], [s[3] for s in seqs], [s[2].blocks() for s in seqs], kv, total, bs)
+        up_bytes, patches, full = gm.last_upload()
+        if prev is None:
+            assert full
+        else:
+            changed = sum(1 for t, p in zip(tables, prev) for i in range(len(t)) if i >= len(p) or t[i] != p[i])
+            assert not full and patches == changed, (step, patches, changed)
+            assert up_bytes == n * 4 + n * 16 + 8 * changed
+        prev = [list(t) for t in tables]
+        for b, s in enumerate(seqs):
+            assert int(am[b]) == orc.argmax(lc[b])
+            assert _rel(lg[b], lc[b]) <= LOGIT_TOL
+            s[4], s[5], s[3] = int(am[b]), orc.argmax(lc[b]), s[3] + 1
+    assert mg.stats()["cow_copies"] == mo.cow_copies == 1
+    got = gm.kv_download()
+    assert np.max(np.abs(got - kv)) <= 1e-4 * np.max(np.abs(kv))
+    gm.close()
