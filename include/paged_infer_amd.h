@@ -282,6 +282,12 @@ int32_t pia_model_decode_path_used(const pia_model* m);
  * batch's layout changed or most slots differ. *bytes = host-to-device bytes of the step,
  * *table_patches = slots patched, *table_full = 1 when the image was re-sent. */
 pia_status pia_model_last_upload(const pia_model* m, int64_t* bytes, int64_t* table_patches, int32_t* table_full);
+/* Diagnostics (no counterpart in the reference): the shared-prefix attention of the last
+ * pia_model_decode. When the entries' tables begin with the same physical blocks (prefix-cache
+ * hits and forks, src/memory/kv_cache_manager.rs:116-327), the K/V of those blocks are read once
+ * per group and kv head instead of once per entry; *virtual_entries = rows of that pass
+ * (0: not used), *shared_splits = its token splits. */
+pia_status pia_model_last_shared(const pia_model* m, int64_t* virtual_entries, int64_t* shared_splits);
 
 /* ------------------------------------------------------------------------------------ */
 /* Sampling (src/sampling.rs).                                                            */

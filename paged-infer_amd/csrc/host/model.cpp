@@ -98,6 +98,7 @@ struct pia_model {
   bool dec_split_on = true;
   int64_t mfma_min = kMfmaMinBatch;
   bool replay_graphs = true;  // diagnostic PIA_NO_GRAPH=1: decode steps launch eagerly
+  bool shared_prefix = true;  // diagnostic PIA_SHARED_PREFIX=0: no shared-prefix attention
   int64_t logit_rows = 0;  // rows of `logits` the last decode / prefill wrote
   DeviceBuffer samp;       // sampling parameters, generator states and drawn tokens
   // Decode block tables, device-resident between steps: entry b's table in slots
@@ -110,6 +111,7 @@ struct pia_model {
   // table image was re-sent.
   int64_t up_bytes = 0, up_patches = 0;
   bool up_full = false;
+  int64_t last_shared = 0, last_shared_splits = 0;  // virtual entries / splits of the last decode's shared prefix
   PinnedBuffer pin, pin_out;
   Prof prof;
 
@@ -123,7 +125,7 @@ struct pia_model {
 
   // Replayable decode / prefill steps. Every kernel argument is a device pointer into the
   // buffers above, so a graph stays valid until one of them is reallocated.
-  std::map<std::array<int64_t, 6>, hipGraphExec_t> graphs;
+  std::map<std::array<int64_t, 8>, hipGraphExec_t> graphs;
 
   ~pia_model() { drop_graphs(); }
 
@@ -279,6 +281,10 @@ struct pia_model {
     const int32_t* tokens;
     const pia_attn_entry* entries;
     const int32_t* tables;
+    // Shared-prefix decode: virtual entries and their (entry, split slot) map, n_shared of them.
+    const pia_attn_entry* shared_entries = nullptr;
+    const int32_t* shared_vmap = nullptr;
+    int64_t n_shared = 0, shared_splits = 0;
   };
 
   // run_layers_batch (src/model.rs:968-1177) for `n` rows whose step inputs are already on the
@@ -303,7 +309,8 @@ struct pia_model {
           launch_rope_kv_write(QKV, ld_qkv, in.entries, in.tables, rope_cos.as<float>(), rope_sin.as<float>(),
                                kv.as<float>(), layout, c.heads, n, l, st());
         AttnLaunch a{QKV, ld_qkv, ATT, ld_h, kv.as<float>(), &layout, c.heads, in.entries, in.tables, n, l, plan,
-                     attn_work.ptr, fused, rope_cos.as<float>(), rope_sin.as<float>(), prefill};
+                     attn_work.ptr, fused, rope_cos.as<float>(), rope_sin.as<float>(), prefill,
+                     in.shared_entries, in.shared_vmap, in.n_shared, in.shared_splits};
         launch_attention(a, st());
       });
       gemv(L.o, ATT, ld_h, nullptr, X, ld_h, n, Epi::Add);
@@ -451,7 +458,7 @@ struct pia_model {
   // first lets the host enqueue ahead so each kernel's events bracket only that kernel), or
   // through a cached graph for `key` (decode steps, replayed every step).
   template <typename F>
-  void run_step(const std::array<int64_t, 6>& key, bool replay, F&& body) {
+  void run_step(const std::array<int64_t, 8>& key, bool replay, F&& body) {
     if (!replay_graphs) replay = false;
     if (!replay && !prof.on) {
       body();
@@ -616,6 +623,7 @@ pia_status pia_model_create(pia_context* ctx, const pia_model_config* cfg, pia_m
   // Diagnostic: PIA_DEC_SPLIT=0 turns the decode GEMM's split K off.
   if (const char* e = std::getenv("PIA_DEC_SPLIT")) m->dec_split_on = std::atoi(e) != 0;
   if (const char* e = std::getenv("PIA_NO_GRAPH")) m->replay_graphs = std::atoi(e) == 0;
+  if (const char* e = std::getenv("PIA_SHARED_PREFIX")) m->shared_prefix = std::atoi(e) != 0;
   *out = m;
   PIA_API_END
 }
@@ -729,6 +737,14 @@ pia_status pia_model_set_decode_path(pia_model* m, int32_t path) {
 }
 
 int32_t pia_model_decode_path_used(const pia_model* m) { return m ? m->last_path : -1; }
+
+pia_status pia_model_last_shared(const pia_model* m, int64_t* virtual_entries, int64_t* shared_splits) {
+  PIA_API_BEGIN
+  PIA_REQUIRE(m, "null model");
+  if (virtual_entries) *virtual_entries = m->last_shared;
+  if (shared_splits) *shared_splits = m->last_shared_splits;
+  PIA_API_END
+}
 
 pia_status pia_model_last_upload(const pia_model* m, int64_t* bytes, int64_t* table_patches, int32_t* table_full) {
   PIA_API_BEGIN
@@ -863,8 +879,16 @@ pia_model::StepDev upload_step(pia_model* m, const std::vector<int32_t>& tok, co
 // travel, as (slot, id) pairs applied by a scatter kernel, unless the layout changed or most
 // slots differ (then the whole image). Host entries index the caller's flat `tables`; the
 // device entries index the resident slots.
+struct SharePlan {
+  std::vector<int32_t> start;         // per entry: first token the per-entry launch covers
+  std::vector<pia_attn_entry> vent;   // virtual entries (table_off = index of the group's first entry)
+  std::vector<int32_t> vmap;          // [vent][2]: entry, split slot
+  int64_t splits = 0;
+};
+
 pia_model::StepDev upload_decode_step(pia_model* m, const std::vector<int32_t>& tok,
-                                      const std::vector<pia_attn_entry>& ent, const int32_t* tables) {
+                                      const std::vector<pia_attn_entry>& ent, const int32_t* tables,
+                                      const SharePlan* sh = nullptr) {
   const int64_t n = static_cast<int64_t>(tok.size());
   int64_t maxlen = 1;
   for (const auto& e : ent) maxlen = std::max<int64_t>(maxlen, e.table_len);
@@ -895,8 +919,19 @@ pia_model::StepDev upload_decode_step(pia_model* m, const std::vector<int32_t>& 
     full = static_cast<int64_t>(patch.size() / 2) * 8 > n * tc;  // most slots changed: send the image
   }
   std::vector<pia_attn_entry> dent(ent);
-  for (int64_t b = 0; b < n; ++b) dent[b].table_off = static_cast<int32_t>(b * tc);
-  const size_t off_e = round_up(n * 4, 256), off_t = off_e + round_up(n * sizeof(pia_attn_entry), 256);
+  for (int64_t b = 0; b < n; ++b) {
+    dent[b].table_off = static_cast<int32_t>(b * tc);
+    if (sh) dent[b].start = sh->start[b];
+  }
+  const int64_t nv = sh ? static_cast<int64_t>(sh->vent.size()) : 0;
+  std::vector<pia_attn_entry> vdev(nv);
+  for (int64_t v = 0; v < nv; ++v) {
+    vdev[v] = sh->vent[v];
+    vdev[v].table_off = static_cast<int32_t>(sh->vent[v].table_off * tc);
+  }
+  const size_t off_v = round_up(n * 4, 256);  // virtual entries and map right after the tokens
+  const size_t off_m = off_v + round_up(nv * sizeof(pia_attn_entry), 256);
+  const size_t off_e = off_m + round_up(nv * 8, 256), off_t = off_e + round_up(n * sizeof(pia_attn_entry), 256);
   const size_t tab_bytes = full ? static_cast<size_t>(n * tc * 4) : patch.size() * 4;
   const size_t total = off_t + round_up(std::max<size_t>(tab_bytes, 4), 256);
   PIA_HIP(hipStreamSynchronize(m->st()));  // the pinned staging buffer may still be in flight
@@ -904,6 +939,10 @@ pia_model::StepDev upload_decode_step(pia_model* m, const std::vector<int32_t>& 
   m->grow(m->step, std::max<size_t>(total, 1 << 16));
   char* p = static_cast<char*>(m->pin.ptr);
   std::memcpy(p, tok.data(), n * 4);
+  if (nv) {
+    std::memcpy(p + off_v, vdev.data(), nv * sizeof(pia_attn_entry));
+    std::memcpy(p + off_m, sh->vmap.data(), nv * 8);
+  }
   std::memcpy(p + off_e, dent.data(), n * sizeof(pia_attn_entry));
   char* d = static_cast<char*>(m->step.ptr);
   if (full) {
@@ -923,11 +962,90 @@ pia_model::StepDev upload_decode_step(pia_model* m, const std::vector<int32_t>& 
                        static_cast<int64_t>(patch.size() / 2), m->st());
     for (size_t i = 0; i < patch.size(); i += 2) m->tab_mirror[patch[i]] = patch[i + 1];
   }
-  m->up_bytes = static_cast<int64_t>(n * 4 + n * sizeof(pia_attn_entry) + tab_bytes);
+  m->up_bytes = static_cast<int64_t>(n * 4 + n * sizeof(pia_attn_entry) + tab_bytes + nv * (sizeof(pia_attn_entry) + 8));
   m->up_patches = static_cast<int64_t>(patch.size() / 2);
   m->up_full = full;
-  return {reinterpret_cast<const int32_t*>(d), reinterpret_cast<const pia_attn_entry*>(d + off_e),
-          m->tab_dev.as<int32_t>()};
+  m->last_shared = nv;
+  m->last_shared_splits = nv ? sh->splits : 0;
+  pia_model::StepDev out{reinterpret_cast<const int32_t*>(d), reinterpret_cast<const pia_attn_entry*>(d + off_e),
+                         m->tab_dev.as<int32_t>()};
+  if (nv) {
+    out.shared_entries = reinterpret_cast<const pia_attn_entry*>(d + off_v);
+    out.shared_vmap = reinterpret_cast<const int32_t*>(d + off_m);
+    out.n_shared = nv;
+    out.shared_splits = sh->splits;
+  }
+  return out;
+}
+
+// Shared-prefix decode plan (src/memory/prefix_cache.rs maps one physical block into many
+// sequences' tables): entries whose tables begin with the same physical blocks form a group;
+// the blocks every member holds at the same logical index, up to the block before each
+// member's current position, are its shared prefix. Their K/V are read once per group by the
+// query-tiled kernel (all members' query heads of one kv head per tile) instead of once per
+// entry; each entry's own launch covers the rest of its window. Used when every entry is in a
+// group with at least kMinSharedTokens shared tokens (no sliding window).
+bool plan_shared_prefix(const pia_model* m, const std::vector<pia_attn_entry>& ent, const int32_t* tables,
+                        SharePlan& sh) {
+  constexpr int64_t kMinSharedTokens = 128;
+  const int64_t n = static_cast<int64_t>(ent.size()), bs = m->layout.block_size;
+  if (n < 2 || m->cfg.attention_window >= 0 || (m->hd != 64 && m->hd != 128)) return false;
+  std::map<int32_t, std::vector<int64_t>> groups;
+  for (int64_t b = 0; b < n; ++b) {
+    if (ent[b].start != 0 || ent[b].table_len < 1) return false;
+    groups[tables[ent[b].table_off]].push_back(b);
+  }
+  const int64_t g = m->cfg.heads / m->cfg.kv_heads;
+  const int64_t qt = attention_tile_rows() / g;  // entries per tile
+  if (qt < 1) return false;
+  const int64_t chunk = m->hd <= 64 ? 64 : 32;
+  std::vector<std::pair<std::vector<int64_t>, int64_t>> gl;  // members, shared tokens
+  int64_t tiles = 0;
+  sh.start.assign(n, 0);
+  for (auto& kv_ : groups) {
+    const auto& mem = kv_.second;
+    if (mem.size() < 2) return false;
+    const pia_attn_entry& f = ent[mem[0]];
+    int64_t blocks = f.table_len;
+    for (int64_t b : mem) {
+      const pia_attn_entry& e = ent[b];
+      blocks = std::min<int64_t>(blocks, std::min<int64_t>(e.table_len, e.pos / bs));
+      int64_t i = 0;
+      while (i < blocks && tables[e.table_off + i] == tables[f.table_off + i]) ++i;
+      blocks = i;
+    }
+    const int64_t len = blocks * bs;
+    if (len < kMinSharedTokens) return false;
+    for (int64_t b : mem) sh.start[b] = static_cast<int32_t>(len);
+    tiles += (static_cast<int64_t>(mem.size()) + qt - 1) / qt;
+    gl.emplace_back(mem, len);
+  }
+  // Shared splits: about two workgroups per CU over (tiles x kv heads x splits).
+  int64_t max_len = 0;
+  for (auto& x : gl) max_len = std::max(max_len, x.second);
+  const int64_t want = (2 * m->ctx->num_cus + tiles * m->cfg.kv_heads - 1) / (tiles * m->cfg.kv_heads);
+  sh.splits = std::max<int64_t>(1, std::min<int64_t>({want, 16, (max_len + chunk - 1) / chunk}));
+  for (auto& x : gl) {
+    const auto& mem = x.first;
+    const int64_t len = x.second;
+    const int64_t per = round_up((len + sh.splits - 1) / sh.splits, chunk);
+    for (int64_t s = 0; s < sh.splits; ++s) {
+      const int64_t a = std::min(len, s * per), b = std::min(len, (s + 1) * per);
+      for (size_t t0 = 0; t0 < mem.size(); t0 += qt)
+        for (int64_t i = 0; i < qt; ++i) {
+          const size_t k = t0 + i;
+          const int64_t who = k < mem.size() ? mem[k] : mem[0];
+          // [a, b): an empty range still writes its (neutral) partials; padding rows (pos -1)
+          // write nothing.
+          const int32_t pos = k < mem.size() ? static_cast<int32_t>(b - 1) : -1;
+          sh.vent.push_back(pia_attn_entry{pos, static_cast<int32_t>(a), static_cast<int32_t>(mem[0]),
+                                           ent[mem[0]].table_len});
+          sh.vmap.push_back(static_cast<int32_t>(who));
+          sh.vmap.push_back(static_cast<int32_t>(s));
+        }
+    }
+  }
+  return true;
 }
 
 int64_t mapped_in_window(const pia_attn_entry& e, int64_t bs) {
@@ -991,22 +1109,35 @@ pia_status pia_model_decode(pia_model* m, const uint32_t* tokens, const int64_t*
   PIA_REQUIRE(ntab == 0 || tables, "null block tables");
   for (int64_t i = 0; i < ntab; ++i)
     PIA_REQUIRE(tables[i] >= 0 && tables[i] < m->layout.num_blocks, "block table entry out of range");
-  const AttnPlan plan = plan_attention(batch, c.kv_heads, m->hd, max_window, m->ctx->num_cus);
   const bool fused = fusable(ent, tables, m->layout.block_size, c.attention_window);
+  SharePlan sh;
+  bool shared = fused && m->shared_prefix && plan_shared_prefix(m, ent, tables, sh);
+  int64_t own_window = max_window;  // tokens the per-entry launch covers
+  if (shared) {
+    own_window = 1;
+    for (int64_t b = 0; b < batch; ++b) own_window = std::max<int64_t>(own_window, ent[b].pos + 1 - sh.start[b]);
+  }
+  AttnPlan plan = plan_attention(batch, c.kv_heads, m->hd, own_window, m->ctx->num_cus);
+  if (shared && plan.splits + sh.splits > 128) {
+    shared = false;
+    sh = SharePlan{};
+    plan = plan_attention(batch, c.kv_heads, m->hd, max_window, m->ctx->num_cus);
+  }
   m->ensure_cap(batch);
   m->ensure_rope(max_pos);
   m->grow(m->logits, batch * m->ld_v * 4);
-  const int64_t wb = attention_work_bytes(batch, c.heads, m->hd, plan.splits);
+  const int64_t wb = attention_work_bytes(batch, c.heads, m->hd, plan.splits + (shared ? sh.splits : 0));
   if (wb) m->grow(m->attn_work, wb);
   const bool step = batch == 1 && m->step_ready() &&
                     max_window <= m->step_shape.max_splits * m->step_shape.max_tokens;
-  const pia_model::StepDev in = upload_decode_step(m, tok, ent, tables);
+  const pia_model::StepDev in = upload_decode_step(m, tok, ent, tables, shared ? &sh : nullptr);
   if (step) {
-    m->run_step({2, 1, 0, 0, 0, 0}, true, [&] {
+    m->run_step({2, 1, 0, 0, 0, 0, 0, 0}, true, [&] {
       m->timed(7, m->step_bytes(mapped), [&] { m->launch_step(in); });
     });
   } else {
-    m->run_step({0, batch, plan.split, plan.splits, plan.chunk, fused ? 1 : 0}, true, [&] {
+    m->run_step({0, batch, plan.split, plan.splits, plan.chunk, fused ? 1 : 0, in.n_shared, in.shared_splits}, true,
+                [&] {
       m->run_layers(batch, in, plan, fused, mapped);
       m->normed_gemv(m->lm_head, m->x.as<float>(), m->final_norm.as<float>(), batch, m->logits.as<float>(), m->ld_v,
                      Epi::Store, m->amax.as<unsigned long long>());
@@ -1054,7 +1185,7 @@ pia_status pia_model_prefill(pia_model* m, const uint32_t* tokens, int64_t n, in
   const int64_t wb = attention_work_bytes(n, c.heads, m->hd, plan.splits);
   if (wb) m->grow(m->attn_work, wb);
   const pia_model::StepDev in = upload_step(m, tok, ent, table, table_len);
-  m->run_step({1, n, plan.split, plan.splits, plan.chunk, fused ? 1 : 0}, false, [&] {
+  m->run_step({1, n, plan.split, plan.splits, plan.chunk, fused ? 1 : 0, 0, 0}, false, [&] {
     m->run_layers(n, in, plan, fused, mapped, true);
     // Only the last position pays for the LM head (src/model.rs:1249-1254).
     m->normed_gemv(m->lm_head, m->x.as<float>() + (n - 1) * m->ld_h, m->final_norm.as<float>(), 1,

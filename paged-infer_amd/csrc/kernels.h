@@ -18,6 +18,16 @@ constexpr int kArgmaxSlots = 256;
 // Batch from which int8 projections run on the matrix cores instead of the streaming GEMV.
 constexpr int64_t kMfmaMinBatch = 5;
 
+// Digit matrix of the matrix-core projection (see gemm_mfma.hip): batch entries in groups of
+// 16, entry b's digit plane j is digit row (3 (b / 16) + j) * 16 + b % 16; storage is k-step
+// major (the 64 bytes of every digit row for one 64-column k-step are contiguous).
+__host__ __device__ inline int digit_row(int b, int j) { return ((b >> 4) * 3 + j) * 16 + (b & 15); }
+__host__ __device__ inline int64_t digit_off(int64_t n, int64_t k, int64_t nrows) {
+  return ((k >> 6) * nrows + n) * 64 + (k & 63);
+}
+// Groups of 16 batch entries: 48 digit rows and 16 power-of-two factors each.
+int64_t digit_groups(int64_t batch);
+
 // Epilogue of a projection: store, accumulate into the destination (residual add, as
 // src/model.rs:1127-1129 and :1165-1167 do with proj_out / ff_down), or SwiGLU over
 // interleaved gate/up row pairs (src/math.rs:293-302).
@@ -123,7 +133,16 @@ struct AttnLaunch {
   // from kPrefillTileMin entries (head_dim 64 or 128, not fused) a query-tiled kernel runs
   // instead, which reads each K/V row once per tile of positions.
   bool prefill = false;
+  // Shared-prefix decode (fused launches only): n_shared virtual entries over the shared
+  // leading blocks of groups of entries (see attention.hip) write their partials into split
+  // slots [0, shared_splits) of `work`; the main launch covers each entry's remaining tokens
+  // (its entry's start) in the slots after them, and the combine merges all of them.
+  const pia_attn_entry* shared_entries = nullptr;
+  const int32_t* shared_vmap = nullptr;  // [n_shared][2]: real entry, split slot
+  int64_t n_shared = 0, shared_splits = 0;
 };
+// Query rows (positions x heads of one kv head) per tile of the shared-prefix / prefill kernel.
+int64_t attention_tile_rows();
 constexpr int64_t kPrefillTileMin = 64;
 void launch_attention(const AttnLaunch& a, hipStream_t st);
 

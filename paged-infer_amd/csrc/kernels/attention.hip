@@ -48,6 +48,9 @@ struct AttnParams {
   const pia_attn_entry* entries;
   const int32_t* tables;
   int split, nsplit, chunk;
+  // Partial outputs of split s go to split slot split_base + s of nstride slots per (entry,
+  // head); the slots below split_base belong to the shared-prefix launch.
+  int split_base, nstride;
   float* part_o;
   float* part_ml;
   const float* rope_cos;
@@ -276,11 +279,11 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnParams p) {
     for (int gr = 0; gr < ngrp; ++gr) acc += red[gr * G * hd + idx];
     const int g = idx / hd, d = idx % hd;
     const int h = kvh * G + g;
-    if (p.nsplit == 1) {
+    if (p.nstride == 1) {
       const float l = stat[4 * g + 1];
       p.out[static_cast<int64_t>(e) * p.ldo + h * hd + d] = l > 0.0f ? acc / l : 0.0f;
     } else {
-      const int64_t ps = (static_cast<int64_t>(e) * p.heads + h) * p.nsplit + s;
+      const int64_t ps = (static_cast<int64_t>(e) * p.heads + h) * p.nstride + p.split_base + s;
       p.part_o[ps * hd + d] = acc;
       if (d == 0) {
         p.part_ml[2 * ps] = stat[4 * g];
@@ -369,7 +372,7 @@ __device__ inline void fma4(float* o, float p, const float4& v) {
 // 2048-token TinyLlama prefills.
 template <int HD>
 constexpr int pf_rows() {
-  return 32;
+  return 32;  // attention_tile_rows()
 }
 // Tokens per chunk: 64, or 32 at head_dim 128 (keeps the LDS of a workgroup near 55 KB so
 // that two or three fit on a CU).
@@ -389,9 +392,21 @@ struct PfParams {
   float scale;
   const pia_attn_entry* entries;
   const int32_t* tables;
+  // Shared-prefix decode (SHARED): entries are virtual, one per (member, shared split) of a
+  // group of decode entries whose tables share their leading blocks; vmap[2 v] is the real
+  // entry whose (raw, un-rotated) q row the virtual entry v reads, vmap[2 v + 1] its split
+  // slot. RoPE at the real entry's position is applied while Q is staged, and the raw
+  // (max, sum, output) partials go to part_ml / part_o as k_attn's splits do.
+  const int* vmap;
+  const pia_attn_entry* real;
+  const float* rope_cos;
+  const float* rope_sin;
+  float* part_o;
+  float* part_ml;
+  int nstride;
 };
 
-template <int G, int HD>
+template <int G, int HD, bool SHARED>
 __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
   constexpr int R = pf_rows<HD>();
   constexpr int kPfChunk = pf_chunk<HD>();
@@ -430,13 +445,36 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
       qstart[i] = 0x7fffffff;
     }
   }
-  for (int i = tid; i < R * (HD / 4); i += kThreads) {
-    const int r = i / (HD / 4), d = (i % (HD / 4)) * 4;
-    const int e = e0 + r / G;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (e < p.n)
-      v = *reinterpret_cast<const float4*>(p.q + static_cast<int64_t>(e) * p.ldq + (kvh * G + r % G) * HD + d);
-    *reinterpret_cast<float4*>(Qs + r * QS + d) = v;
+  if constexpr (SHARED) {
+    // NeoX RoPE at each real entry's position (src/math.rs:343-367), as the fused decode
+    // kernel applies it to the same raw q rows.
+    constexpr int half = HD / 2;
+    for (int i = tid; i < R * half; i += kThreads) {
+      const int r = i / half, j = i % half;
+      const int e = e0 + r / G;
+      float a = 0.0f, b = 0.0f;
+      if (e < p.n) {
+        const int er = p.vmap[2 * e];
+        const int pos = p.real[er].pos;
+        const float* qh = p.q + static_cast<int64_t>(er) * p.ldq + (kvh * G + r % G) * HD;
+        const float c = p.rope_cos[static_cast<int64_t>(pos) * half + j];
+        const float sn = p.rope_sin[static_cast<int64_t>(pos) * half + j];
+        const float x0 = qh[j], x1 = qh[j + half];
+        a = x0 * c - x1 * sn;
+        b = x1 * c + x0 * sn;
+      }
+      Qs[r * QS + j] = a;
+      Qs[r * QS + j + half] = b;
+    }
+  } else {
+    for (int i = tid; i < R * (HD / 4); i += kThreads) {
+      const int r = i / (HD / 4), d = (i % (HD / 4)) * 4;
+      const int e = e0 + r / G;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (e < p.n)
+        v = *reinterpret_cast<const float4*>(p.q + static_cast<int64_t>(e) * p.ldq + (kvh * G + r % G) * HD + d);
+      *reinterpret_cast<float4*>(Qs + r * QS + d) = v;
+    }
   }
   __syncthreads();
   int lo = 0x7fffffff, hi = -1;
@@ -610,6 +648,24 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
     __syncthreads();  // Ks / Vs / Ps are rewritten by the next chunk
   }
 
+  if constexpr (SHARED) {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int r = rg * RPT + i;
+      const int e = e0 + r / G;
+      if (e >= p.n || qpos[r / G] < 0) continue;
+      const int64_t ps = (static_cast<int64_t>(p.vmap[2 * e]) * p.heads + kvh * G + r % G) * p.nstride + p.vmap[2 * e + 1];
+#pragma unroll
+      for (int w = 0; w < W; ++w)
+        *reinterpret_cast<float4*>(p.part_o + ps * HD + tg * 4 + 64 * w) =
+            make_float4(o[i][w][0], o[i][w][1], o[i][w][2], o[i][w][3]);
+      if (tg == 0) {
+        p.part_ml[2 * ps] = m[i];
+        p.part_ml[2 * ps + 1] = l[i];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
     const int r = rg * RPT + i;
@@ -636,28 +692,28 @@ size_t pf_smem_bytes() {
          sizeof(int) * (2 * kPfChunk + 2 * R);
 }
 
-template <int G, int HD>
+template <int G, int HD, bool SHARED>
 void go_prefill(const PfParams& p, hipStream_t st) {
   constexpr int QT = pf_rows<HD>() / G;
   const size_t smem = pf_smem_bytes<HD>();
   static bool done = false;
   if (!done) {
-    PIA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_prefill<G, HD>),
+    PIA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_prefill<G, HD, SHARED>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
     done = true;
   }
   dim3 grid(static_cast<unsigned>((p.n + QT - 1) / QT), static_cast<unsigned>(p.hkv));
-  hipLaunchKernelGGL((k_attn_prefill<G, HD>), grid, dim3(kThreads), smem, st, p);
+  hipLaunchKernelGGL((k_attn_prefill<G, HD, SHARED>), grid, dim3(kThreads), smem, st, p);
 }
 
-template <int HD>
+template <int HD, bool SHARED = false>
 void prefill_by_g(const PfParams& p, int g, hipStream_t st) {
   switch (g) {
-    case 1: go_prefill<1, HD>(p, st); break;
-    case 2: go_prefill<2, HD>(p, st); break;
-    case 4: go_prefill<4, HD>(p, st); break;
-    case 8: go_prefill<8, HD>(p, st); break;
-    case 16: go_prefill<16, HD>(p, st); break;
+    case 1: go_prefill<1, HD, SHARED>(p, st); break;
+    case 2: go_prefill<2, HD, SHARED>(p, st); break;
+    case 4: go_prefill<4, HD, SHARED>(p, st); break;
+    case 8: go_prefill<8, HD, SHARED>(p, st); break;
+    case 16: go_prefill<16, HD, SHARED>(p, st); break;
     default: fail(PIA_ERR_INVALID, "attention: kv_group must be 1, 2, 4, 8 or 16");
   }
 }
@@ -747,6 +803,8 @@ AttnPlan plan_attention(int64_t n, int64_t num_kv_heads, int64_t head_dim, int64
   return plan;
 }
 
+int64_t attention_tile_rows() { return 32; }
+
 int64_t attention_work_bytes(int64_t n, int64_t heads, int64_t head_dim, int64_t splits) {
   if (splits <= 1) return 0;
   return n * heads * splits * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
@@ -801,8 +859,21 @@ void launch_attention(const AttnLaunch& a, hipStream_t st) {
   p.split = static_cast<int>(a.plan.split);
   p.chunk = static_cast<int>(a.plan.chunk);
   p.nsplit = static_cast<int>(a.plan.splits);
+  p.split_base = static_cast<int>(a.n_shared ? a.shared_splits : 0);
+  p.nstride = p.split_base + p.nsplit;
   p.part_o = static_cast<float*>(a.work);
-  p.part_ml = p.part_o ? p.part_o + a.n * a.heads * a.plan.splits * hd : nullptr;
+  p.part_ml = p.part_o ? p.part_o + a.n * a.heads * p.nstride * hd : nullptr;
+  if (a.n_shared) {
+    PIA_REQUIRE(a.fused && !a.prefill && (hd == 64 || hd == 128) && a.shared_entries && a.shared_vmap && a.work &&
+                    a.shared_splits >= 1 && p.nstride <= kThreads / 2,
+                "attention: shared-prefix decode needs a fused launch, head_dim 64 or 128 and a workspace");
+    PfParams sp{a.q, a.ldq, nullptr, 0, a.kv, p.layer_slots, p.block_size, p.hkv, p.heads,
+                static_cast<int>(a.n_shared), p.scale, a.shared_entries, a.tables, a.shared_vmap, a.entries,
+                a.rope_cos, a.rope_sin, p.part_o, p.part_ml, p.nstride};
+    if (hd == 64) prefill_by_g<64, true>(sp, g, st);
+    else prefill_by_g<128, true>(sp, g, st);
+    PIA_HIP(hipGetLastError());
+  }
   p.rope_cos = a.rope_cos;
   p.rope_sin = a.rope_sin;
   dim3 grid(static_cast<unsigned>(a.plan.splits), static_cast<unsigned>(L.num_kv_heads), static_cast<unsigned>(a.n));
@@ -816,9 +887,9 @@ void launch_attention(const AttnLaunch& a, hipStream_t st) {
     default: fail(PIA_ERR_INVALID, "attention: kv_group must be 1, 2, 4, 8 or 16");
   }
   PIA_HIP(hipGetLastError());
-  if (a.plan.splits > 1) {
+  if (p.nstride > 1) {
     hipLaunchKernelGGL(k_attn_combine, dim3(static_cast<unsigned>(a.n * a.heads)), dim3(kMaxHd), 0, st, p.part_o,
-                       p.part_ml, a.out, a.ldo, static_cast<int>(a.heads), hd, static_cast<int>(a.plan.splits));
+                       p.part_ml, a.out, a.ldo, static_cast<int>(a.heads), hd, p.nstride);
     PIA_HIP(hipGetLastError());
   }
 }

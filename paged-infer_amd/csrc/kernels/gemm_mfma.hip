@@ -36,12 +36,7 @@ constexpr int64_t kDecTargetGroups = 256;
 constexpr int64_t kDecMinSteps = 8;  // 64-byte k-steps per slice, at least
 constexpr int64_t kDecMaxSplit = 8;
 
-__host__ __device__ inline int digit_row(int b, int j) { return ((b >> 4) * 3 + j) * 16 + (b & 15); }
-// Byte offset of digit row n, column k in a digit matrix of nrows rows: k-step major (the 64
-// bytes of every row for one k-step are contiguous, so a k-step's digit tile is one block).
-__host__ __device__ inline int64_t digit_off(int64_t n, int64_t k, int64_t nrows) {
-  return ((k >> 6) * nrows + n) * 64 + (k & 63);
-}
+
 
 __device__ inline float block_reduce_sum(float v, float* red) {
 #pragma unroll
@@ -735,7 +730,6 @@ void go_tile(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int 
 
 }  // namespace
 
-// Groups of 16 batch entries: 48 digit rows and 16 power-of-two factors each.
 int64_t digit_groups(int64_t batch) { return (batch + 15) / 16; }
 
 int64_t xdigits_bytes(int64_t batch, int64_t cols) {

@@ -156,6 +156,7 @@ _SIGS = {
     "pia_model_set_decode_path": (I32, [P, I32]),
     "pia_model_decode_path_used": (I32, [P]),
     "pia_model_last_upload": (I32, [P, P, P, P]),
+    "pia_model_last_shared": (I32, [P, P, P]),
     "pia_model_profile_get": (I32, [P, P, P, P, I32]),
     "pia_model_bench_class": (I32, [P, I32, I64, I32, C.POINTER(C.c_double), C.POINTER(I64)]),
     "pia_bench_projection": (I32, [P, I64, I64, I64, I32, I32, C.POINTER(C.c_double), C.POINTER(I64)]),
@@ -672,6 +673,12 @@ class Model:
         b, pch, full = I64(), I64(), I32()
         check(lib().pia_model_last_upload(self.h, C.byref(b), C.byref(pch), C.byref(full)))
         return b.value, pch.value, bool(full.value)
+
+    def last_shared(self):
+        """(virtual entries, splits) of the last decode's shared-prefix attention (0: not used)."""
+        v, sp = I64(), I64()
+        check(lib().pia_model_last_shared(self.h, C.byref(v), C.byref(sp)))
+        return v.value, sp.value
 
     def profile_get(self):
         """(ms, algorithmic bytes, launches) per class of the last profiled call."""

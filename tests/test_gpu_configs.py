@@ -193,3 +193,61 @@ def test_config5_llama3_batch64_prefix_sharing_cow(ctx):
     assert np.array_equal(got[:, ~written], ref[:, ~written])
     assert np.max(np.abs(got[:, written] - ref[:, written])) <= KV_TOL * np.max(np.abs(ref))
     gm.close()
+
+
+def test_shared_prefix_decode_uneven_groups(ctx):
+    """Decode entries whose block tables begin with the same physical blocks (prefix-cache hits
+    and forks) read the shared K/V once per group: groups of 3, 5 and 2 entries (tiles of 4
+    query positions at 8 heads per kv head, so padded tiles), one member of the 5-group diverging
+    after 9 of its group's 11 blocks (the group's shared prefix stops there), positions in
+    different blocks. Logits
+    and greedy tokens vs the oracle (which reads every entry's window in full), with the
+    shared pass on, and the same decode with it off."""
+    cfg = pia.LlamaConfig(hidden=1024, layers=2, heads=16, kv_heads=2, inter=512, vocab=1024)
+    bs = 16
+    rng = np.random.default_rng(44)
+    w = pia.synth_weights(cfg, seed=44)
+    nb = 200
+    pool = rng.permutation(nb).tolist()
+    take = lambda k: [pool.pop() for _ in range(k)]
+    tables, pos = [], []
+    for size, shared_blocks in ((3, 10), (5, 11), (2, 12)):
+        prefix = take(shared_blocks)
+        for i in range(size):
+            own = take(4)
+            t = list(prefix) + own
+            if size == 5 and i == 4:
+                t = prefix[:9] + take(2) + own  # diverges after 9 shared blocks
+            tables.append(t)
+            pos.append(len(t) * bs - 1 - int(rng.integers(0, 3 * bs)))
+    n = len(tables)
+    kv = (rng.standard_normal(orc.kv_floats(cfg, nb, bs), dtype=np.float32) * 0.5)
+    gm = pia.Model(ctx, cfg, w)
+    gm.kv_alloc(nb, bs)
+    gm.kv_upload(kv)
+    om_ = orc.OracleModel(cfg, w)
+    toks = rng.integers(0, cfg.vocab, n).tolist()
+    lg, am = gm.decode(toks, pos, tables)
+    nvirt, splits = gm.last_shared()
+    lc = om_.decode(toks, pos, tables, kv, nb, bs)
+    rel = max(_rel(lg[b], lc[b]) for b in range(n))
+    _say(f"[shared-prefix] virtual rows {nvirt}, splits {splits}, rel={rel:.3g}")
+    assert nvirt > 0 and splits >= 1
+    assert rel <= LOGIT_TOL
+    assert am.tolist() == [orc.argmax(r) for r in lc]
+    # The same step without the shared pass (fresh cache: the first decode wrote its tokens).
+    gm.kv_upload(kv)
+    import os
+    os.environ["PIA_SHARED_PREFIX"] = "0"
+    try:
+        g2 = pia.Model(ctx, cfg, w)
+    finally:
+        del os.environ["PIA_SHARED_PREFIX"]
+    g2.kv_alloc(nb, bs)
+    g2.kv_upload(kv)
+    l2, a2 = g2.decode(toks, pos, tables)
+    assert g2.last_shared()[0] == 0
+    assert a2.tolist() == am.tolist()
+    assert max(_rel(lg[b], l2[b]) for b in range(n)) <= LOGIT_TOL
+    g2.close()
+    gm.close()
