@@ -589,7 +589,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 // waves, each 64 rows x 96 columns = 2 x 3 tiles of v_mfma_i32_32x32x32_i8.
 namespace tile {
 constexpr int kBM = 128, kBN = 192, kBK = 64;
-constexpr int kPitch = kBK + 16;  // LDS row pitch in bytes (staggers rows across banks)
+constexpr int kPitch = kBK;  // LDS row pitch in bytes; 16-byte chunks swizzled (dec::chunk_pos)
 constexpr int kStage = (kBM + kBN) * kPitch;
 constexpr int kWLoads = kBM * kBK / 16 / kThreads;  // 16-byte loads per thread per stage: 2
 constexpr int kDLoads = kBN * kBK / 16 / kThreads;  // 3
@@ -632,9 +632,11 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const int8_t* __restrict
     int8_t* ws = lds + buf * kStage;
     int8_t* ds = ws + kBM * kPitch;
 #pragma unroll
-    for (int u = 0; u < kWLoads; ++u) *reinterpret_cast<v4i*>(ws + (trow + 64 * u) * kPitch + seg * 16) = wreg[u];
+    for (int u = 0; u < kWLoads; ++u)
+      *reinterpret_cast<v4i*>(ws + (trow + 64 * u) * kPitch + dec::chunk_pos(trow + 64 * u, seg)) = wreg[u];
 #pragma unroll
-    for (int u = 0; u < kDLoads; ++u) *reinterpret_cast<v4i*>(ds + (trow + 64 * u) * kPitch + seg * 16) = dreg[u];
+    for (int u = 0; u < kDLoads; ++u)
+      *reinterpret_cast<v4i*>(ds + (trow + 64 * u) * kPitch + dec::chunk_pos(trow + 64 * u, seg)) = dreg[u];
   };
 
   v16i acc[2][3];
@@ -659,10 +661,12 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const int8_t* __restrict
       v4i a[2], b[3];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        a[i] = *reinterpret_cast<const v4i*>(ws + (wr * 64 + i * 32 + r_l) * kPitch + kk + kh * 16);
+        a[i] = *reinterpret_cast<const v4i*>(ws + (wr * 64 + i * 32 + r_l) * kPitch +
+                                             dec::chunk_pos(r_l, kk / 16 + kh));
 #pragma unroll
       for (int j = 0; j < 3; ++j)
-        b[j] = *reinterpret_cast<const v4i*>(ds + (wc * 96 + j * 32 + r_l) * kPitch + kk + kh * 16);
+        b[j] = *reinterpret_cast<const v4i*>(ds + (wc * 96 + j * 32 + r_l) * kPitch +
+                                             dec::chunk_pos(r_l, kk / 16 + kh));
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
