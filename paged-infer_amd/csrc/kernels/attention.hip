@@ -349,37 +349,23 @@ __global__ __launch_bounds__(kMaxHd) void k_attn_combine(const float* __restrict
 // ---------------------------------------------------------------------------------------
 // Prefill attention: the entries of one launch are consecutive positions of one sequence
 // sharing one block table (prefill_batched, src/model.rs:1222-1255), and their K/V are
-// already in the cache. A workgroup owns R query rows of one kv head (QT = R / G
-// consecutive positions times the G heads of the group, row r = query (r / G), head
-// kvh * G + r % G) and walks the tokens its positions attend to in chunks of kPfChunk,
-// staged in LDS, so each K and V row is read once per R rows instead of once per G.
-// Scores, online softmax and P.V run on register tiles: thread (rg, tg) owns rows
-// rg * RPT .. + RPT and, per chunk, the tokens tg + 16 j (scores) or the dims tg * 4 + 64 w
-// (output). The next chunk's block ids are resolved during the scores and its K/V loads
-// are in flight during P.V.
-constexpr int kPfPad = 4;  // floats of padding per LDS row of Q, K and P (bank spread)
+// already in the cache. The same kernel runs the shared-prefix decode pass (SHARED).
+//
+// A workgroup owns kRowsTile = 64 query rows of one kv head, 16 per wave: row r is query
+// r / G, head kvh * G + r % G (QT = 64 / G consecutive positions times the G heads of the
+// group). It walks the tokens its positions attend to in chunks of kRc, staged in LDS, so each
+// K and V row is read once per 64 rows instead of once per G; the next chunk's block ids are
+// resolved and its K/V loads are in flight during the current chunk. Per wave and chunk the
+// scores are formed transposed, S^T = K Q^T, on the f32 matrix cores (v_mfma_f32_16x16x4f32;
+// each lane's dims are one contiguous quarter of the head, so its K reads are 16-byte and the
+// dot is the same sum in another order). In that layout the lane holding a score is the lane
+// that feeds it to P.V as the A operand, so softmax and P.V run from registers with no round
+// trip of P through LDS. The output dims are permuted per lane (column c holds dims
+// c * HD / 16 ..) so V is read in 16-byte pieces too; the per-row rescale factors reach the
+// output layout by shuffles.
+constexpr int kRowsTile = 64;
+constexpr int kPfPad = 4;  // floats of padding per LDS row of K and V (bank spread)
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-__device__ inline void fma4(float* o, float p, const float4& v) {
-  o[0] = __builtin_fmaf(p, v.x, o[0]);
-  o[1] = __builtin_fmaf(p, v.y, o[1]);
-  o[2] = __builtin_fmaf(p, v.z, o[2]);
-  o[3] = __builtin_fmaf(p, v.w, o[3]);
-}
-
-// Query-head rows per workgroup. Taller tiles reuse each K/V row more but their LDS and
-// registers leave fewer waves per CU to hide LDS latency: 32 measured best of 16/32/64/128 on
-// 2048-token TinyLlama prefills.
-template <int HD>
-constexpr int pf_rows() {
-  return 32;  // attention_tile_rows()
-}
-// Tokens per chunk: 64, or 32 at head_dim 128 (keeps the LDS of a workgroup near 55 KB so
-// that two or three fit on a CU).
-template <int HD>
-constexpr int pf_chunk() {
-  return HD <= 64 ? 64 : 32;
-}
 
 struct PfParams {
   const float* q;  // rows [n][ldq]: head h at column h * hd (post-RoPE)
@@ -406,31 +392,35 @@ struct PfParams {
   int nstride;
 };
 
+template <int HD>
+constexpr int rows_chunk() {
+  return HD <= 64 ? 64 : 32;
+}
+
 template <int G, int HD, bool SHARED>
 __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
-  constexpr int R = pf_rows<HD>();
-  constexpr int kPfChunk = pf_chunk<HD>();
-  constexpr int TJ = kPfChunk / 16;  // tokens per thread in the scores
-  constexpr int QT = R / G;         // query positions per workgroup
-  constexpr int RPT = R / 16;       // rows per thread
-  constexpr int QS = HD + kPfPad;   // LDS row stride of Q and K
-  constexpr int PS = kPfChunk + kPfPad;
-  constexpr int W = HD / 64;        // float4 dim groups per thread in P.V (dims tg*4 + 64 w)
-  constexpr int KV4 = kPfChunk * HD / 4 / kThreads;  // float4 of K (and of V) per thread per chunk
-  static_assert(HD % 64 == 0 && R % 16 == 0 && QT >= 1 && KV4 >= 1, "prefill attention tile shape");
+  constexpr int R = kRowsTile;        // query rows per workgroup
+  constexpr int QT = R / G;           // query positions per workgroup
+  constexpr int kRc = rows_chunk<HD>();
+  constexpr int TT = kRc / 16;        // token tiles per chunk
+  constexpr int DQ = HD / 4;          // dims per lane quarter in S^T
+  constexpr int DT = HD / 16;         // output dim tiles (dims per lane column)
+  constexpr int KS = HD + kPfPad;     // LDS row stride of K and V (floats)
+  constexpr int KV4 = kRc * HD / 4 / kThreads;  // float4 of K (and of V) per thread per chunk
+  static_assert(HD % 64 == 0 && QT >= 1 && KV4 >= 1 && kThreads == 256, "row-tiled attention shape");
   extern __shared__ __align__(16) float smem[];
-  float* Qs = smem;                  // [R][QS]
-  float* Ks = Qs + R * QS;           // [kPfChunk][QS]
-  float* Vs = Ks + kPfChunk * QS;    // [kPfChunk][HD]
-  float* Ps = Vs + kPfChunk * HD;    // [R][PS]
-  int* slots = reinterpret_cast<int*>(Ps + R * PS);  // [2][kPfChunk]
-  int* qpos = slots + 2 * kPfChunk;  // [QT]
-  int* qstart = qpos + QT;           // [QT]
+  float* Ks = smem;                    // [kRc][KS]
+  float* Vs = Ks + kRc * KS;           // [kRc][KS]
+  float* qstage = smem;                // [R][HD] query rows, before the first chunk only
+  static_assert(2 * kRc * KS >= R * HD, "the query rows are staged where K/V go");
+  int* slots = reinterpret_cast<int*>(Vs + kRc * KS);  // [2][kRc]
+  int* qpos = slots + 2 * kRc;         // [QT]
+  int* qstart = qpos + QT;             // [QT]
 
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j16 = lane & 15, q4 = lane >> 4;
   const int kvh = blockIdx.y;
-  // The longest windows (last positions) first: they take the most chunks.
-  const int tile = gridDim.x - 1 - blockIdx.x;
+  const int tile = gridDim.x - 1 - blockIdx.x;  // longest windows first
   const int e0 = tile * QT;
   const pia_attn_entry first = p.entries[e0];
   const int table_off = first.table_off, table_len = first.table_len;
@@ -441,30 +431,28 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
       qpos[i] = en.pos;
       qstart[i] = en.start;
     } else {
-      qpos[i] = -1;  // no such query: every token masked, nothing written
+      qpos[i] = -1;
       qstart[i] = 0x7fffffff;
     }
   }
   if constexpr (SHARED) {
-    // NeoX RoPE at each real entry's position (src/math.rs:343-367), as the fused decode
-    // kernel applies it to the same raw q rows.
     constexpr int half = HD / 2;
     for (int i = tid; i < R * half; i += kThreads) {
-      const int r = i / half, j = i % half;
+      const int r = i / half, jj = i % half;
       const int e = e0 + r / G;
       float a = 0.0f, b = 0.0f;
       if (e < p.n) {
         const int er = p.vmap[2 * e];
         const int pos = p.real[er].pos;
         const float* qh = p.q + static_cast<int64_t>(er) * p.ldq + (kvh * G + r % G) * HD;
-        const float c = p.rope_cos[static_cast<int64_t>(pos) * half + j];
-        const float sn = p.rope_sin[static_cast<int64_t>(pos) * half + j];
-        const float x0 = qh[j], x1 = qh[j + half];
+        const float c = p.rope_cos[static_cast<int64_t>(pos) * half + jj];
+        const float sn = p.rope_sin[static_cast<int64_t>(pos) * half + jj];
+        const float x0 = qh[jj], x1 = qh[jj + half];
         a = x0 * c - x1 * sn;
         b = x1 * c + x0 * sn;
       }
-      Qs[r * QS + j] = a;
-      Qs[r * QS + j + half] = b;
+      qstage[r * HD + jj] = a;
+      qstage[r * HD + jj + half] = b;
     }
   } else {
     for (int i = tid; i < R * (HD / 4); i += kThreads) {
@@ -473,7 +461,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (e < p.n)
         v = *reinterpret_cast<const float4*>(p.q + static_cast<int64_t>(e) * p.ldq + (kvh * G + r % G) * HD + d);
-      *reinterpret_cast<float4*>(Qs + r * QS + d) = v;
+      *reinterpret_cast<float4*>(qstage + r * HD + d) = v;
     }
   }
   __syncthreads();
@@ -481,11 +469,21 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
   for (int i = 0; i < QT; ++i)
     if (qpos[i] >= 0) lo = min(lo, qstart[i]), hi = max(hi, qpos[i]);
   if (hi < 0) return;  // uniform over the workgroup
-  const int nchunks = hi >= lo ? (hi - lo) / kPfChunk + 1 : 0;
+  const int nchunks = hi >= lo ? (hi - lo) / kRc + 1 : 0;
 
-  auto resolve = [&](int c, int* dst) {  // block ids of chunk c (threads < kPfChunk)
-    if (tid < kPfChunk) {
-      const int t = lo + c * kPfChunk + tid;
+  // This lane's row (S^T layout) and its query quarter of dims, in registers.
+  const int row = wave * 16 + j16;
+  const int rpos = qpos[row / G], rstart = qstart[row / G];
+  float qv[DQ];
+#pragma unroll
+  for (int m = 0; m < DQ; m += 4) {
+    const float4 v = *reinterpret_cast<const float4*>(qstage + row * HD + q4 * DQ + m);
+    qv[m] = v.x, qv[m + 1] = v.y, qv[m + 2] = v.z, qv[m + 3] = v.w;
+  }
+
+  auto resolve = [&](int c, int* dst) {
+    if (tid < kRc) {
+      const int t = lo + c * kRc + tid;
       int slot = -1;
       if (t <= hi) {
         const int lb = t / p.block_size;
@@ -495,32 +493,30 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
     }
   };
   const int64_t head_stride = 2 * static_cast<int64_t>(HD);
+  // The loads stay raw in registers while in flight; unmapped tokens (which read slot 0 of the
+  // layer, always inside the cache) are zeroed when the chunk is written to LDS.
   float4 kreg[KV4], vreg[KV4];
+  bool kept[KV4];
   auto load = [&](const int* sl) {
 #pragma unroll
     for (int u = 0; u < KV4; ++u) {
       const int i = tid + u * kThreads;
       const int t = i / (HD / 4), d = (i % (HD / 4)) * 4;
-      // Unmapped tokens read slot 0 of the layer (always inside the cache) and are zeroed.
       const int slot = sl[t];
       const float* src = p.kv + ((p.layer_slots + max(slot, 0)) * p.hkv + kvh) * head_stride + d;
-      const float4 k4 = *reinterpret_cast<const float4*>(src);
-      const float4 v4 = *reinterpret_cast<const float4*>(src + HD);
-      const bool keep = slot >= 0;
-      kreg[u] = make_float4(keep ? k4.x : 0.f, keep ? k4.y : 0.f, keep ? k4.z : 0.f, keep ? k4.w : 0.f);
-      vreg[u] = make_float4(keep ? v4.x : 0.f, keep ? v4.y : 0.f, keep ? v4.z : 0.f, keep ? v4.w : 0.f);
+      kreg[u] = *reinterpret_cast<const float4*>(src);
+      vreg[u] = *reinterpret_cast<const float4*>(src + HD);
+      kept[u] = slot >= 0;
     }
   };
+  auto zero_unless = [](bool keep, const float4& x) {
+    return make_float4(keep ? x.x : 0.f, keep ? x.y : 0.f, keep ? x.z : 0.f, keep ? x.w : 0.f);
+  };
 
-  const int rg = tid / 16, tg = tid % 16;
-  float m[RPT], l[RPT], o[RPT][W][4];
+  float m = -INFINITY, lsum = 0.0f;  // this lane's row: running max, partial sum over its tokens
+  f32x4 acc[DT];                     // O rows 4 * q4 + v, dims j16 * DT + dt
 #pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    m[i] = -INFINITY;
-    l[i] = 0.0f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) o[i][w][0] = o[i][w][1] = o[i][w][2] = o[i][w][3] = 0.0f;
-  }
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (nchunks > 0) {
     resolve(0, slots);
@@ -528,174 +524,129 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
     load(slots);
   }
   for (int c = 0; c < nchunks; ++c) {
-    const int* cur = slots + (c & 1) * kPfChunk;
-    int* nxt = slots + ((c + 1) & 1) * kPfChunk;
-    const int c0 = lo + c * kPfChunk;
+    const int* cur = slots + (c & 1) * kRc;
+    int* nxt = slots + ((c + 1) & 1) * kRc;
+    const int c0 = lo + c * kRc;
 #pragma unroll
     for (int u = 0; u < KV4; ++u) {
       const int i = tid + u * kThreads;
       const int t = i / (HD / 4), d = (i % (HD / 4)) * 4;
-      *reinterpret_cast<float4*>(Ks + t * QS + d) = kreg[u];
-      *reinterpret_cast<float4*>(Vs + t * HD + d) = vreg[u];
+      *reinterpret_cast<float4*>(Ks + t * KS + d) = zero_unless(kept[u], kreg[u]);
+      *reinterpret_cast<float4*>(Vs + t * KS + d) = zero_unless(kept[u], vreg[u]);
     }
     __syncthreads();
     if (c + 1 < nchunks) resolve(c + 1, nxt);
-
-    // Scores on the f32 matrix cores: wave w computes TPW 16x16 tiles of S = Q K^T (rows
-    // rt*16.., tokens tt*16..), the head dimension split into four contiguous quarters, one
-    // per 16-lane group (any order of the dot product's terms is the same sum, rounded
-    // differently). S goes to Ps, then each thread reads its (row, token) elements.
-    {
-      constexpr int NTT = kPfChunk / 16;           // token tiles per chunk
-      static_assert(kThreads == 256, "the score tiles are split over exactly four waves");
-      constexpr int TPW = (R / 16) * NTT / 4;      // tiles per wave
-      constexpr int KL = HD / 4;                   // head dims per lane group
-      static_assert(TPW >= 1 && (R / 16) * NTT % 4 == 0 && NTT % TPW == 0, "score tiles per wave");
-      const int wave = tid >> 6, lane = tid & 63, lr = lane & 15, kq = lane >> 4;
-      const int tile0 = wave * TPW, rt = tile0 / NTT;
-      f32x4 acc[TPW];
+    // S^T tiles: token tt * 16 + 4 q4 + v, row j16 of this wave.
+    // The TT tiles' dependency chains are interleaved so consecutive MFMAs are independent.
+    f32x4 st[TT];
 #pragma unroll
-      for (int j = 0; j < TPW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const float* qa = Qs + (rt * 16 + lr) * QS + kq * KL;
+    for (int tt = 0; tt < TT; ++tt) st[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const float* kr = Ks + j16 * KS + q4 * DQ;
 #pragma unroll
-      for (int k4 = 0; k4 < KL; k4 += 4) {
-        const float4 a = *reinterpret_cast<const float4*>(qa + k4);
-        float4 b[TPW];
+    for (int m4 = 0; m4 < DQ; m4 += 4) {
+      float4 k4[TT];
 #pragma unroll
-        for (int j = 0; j < TPW; ++j)
-          b[j] = *reinterpret_cast<const float4*>(Ks + (((tile0 + j) % NTT) * 16 + lr) * QS + kq * KL + k4);
+      for (int tt = 0; tt < TT; ++tt) k4[tt] = *reinterpret_cast<const float4*>(kr + tt * 16 * KS + m4);
 #pragma unroll
-        for (int j = 0; j < TPW; ++j) {
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b[j].x, acc[j], 0, 0, 0);
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b[j].y, acc[j], 0, 0, 0);
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b[j].z, acc[j], 0, 0, 0);
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b[j].w, acc[j], 0, 0, 0);
-        }
-      }
-      // Result layout: lane holds rows 4 * (lane / 16) + v of the tile, token lane % 16.
+      for (int tt = 0; tt < TT; ++tt) st[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[tt].x, qv[m4], st[tt], 0, 0, 0);
 #pragma unroll
-      for (int j = 0; j < TPW; ++j) {
-        const int tt = (tile0 + j) % NTT;
+      for (int tt = 0; tt < TT; ++tt) st[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[tt].y, qv[m4 + 1], st[tt], 0, 0, 0);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) Ps[(rt * 16 + 4 * kq + v) * PS + tt * 16 + lr] = acc[j][v];
-      }
+      for (int tt = 0; tt < TT; ++tt) st[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[tt].z, qv[m4 + 2], st[tt], 0, 0, 0);
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) st[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[tt].w, qv[m4 + 3], st[tt], 0, 0, 0);
     }
-    __syncthreads();
-    float s[RPT][TJ];
+    // Mask, scale, running max over the row (the 4 lanes j16 + 16 q share a row).
+    float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < RPT; ++i)
+    for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) s[i][j] = Ps[(rg * RPT + i) * PS + tg + 16 * j];
-    float alpha[RPT];
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const int r = rg * RPT + i;
-      const int pos = qpos[r / G], st = qstart[r / G];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) {
-        const int tk = tg + 16 * j;
+      for (int v = 0; v < 4; ++v) {
+        const int tk = tt * 16 + 4 * q4 + v;
         const int t = c0 + tk;
-        const bool ok = cur[tk] >= 0 && t >= st && t <= pos;
-        s[i][j] = ok ? s[i][j] * p.scale : -INFINITY;
-        mx = fmaxf(mx, s[i][j]);
+        const bool ok = cur[tk] >= 0 && t >= rstart && t <= rpos;
+        st[tt][v] = ok ? st[tt][v] * p.scale : -INFINITY;
+        mx = fmaxf(mx, st[tt][v]);
       }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float alpha = (m == -INFINITY) ? 1.0f : expf(m - m_new);
+    float ps = 0.0f;
 #pragma unroll
-      for (int off = 8; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-      const float m_new = fmaxf(m[i], mx);
-      float sum = 0.0f;
+    for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) {
-        const float pr = (m_new == -INFINITY) ? 0.0f : expf(s[i][j] - m_new);
-        Ps[r * PS + tg + 16 * j] = pr;
-        sum += pr;
+      for (int v = 0; v < 4; ++v) {
+        const float pr = (m_new == -INFINITY) ? 0.0f : expf(st[tt][v] - m_new);
+        st[tt][v] = pr;
+        ps += pr;
       }
-#pragma unroll
-      for (int off = 8; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
-      alpha[i] = (m[i] == -INFINITY) ? 0.0f : expf(m[i] - m_new);
-      l[i] = __builtin_fmaf(l[i], alpha[i], sum);
-      m[i] = m_new;
-    }
-    __syncthreads();  // P complete; the next chunk's block ids resolved
+    lsum = __builtin_fmaf(lsum, alpha, ps);
+    m = m_new;
+    __syncthreads();  // every wave has read Ks; the next chunk's block ids are resolved
     if (c + 1 < nchunks) load(nxt);
-
-    // O[r][d] = O * alpha + sum_t P[r][t] V[t][d], dims tg*4 + 64 w.
+    // Output rows 4 q4 + v take the factor of the lane that owns that row in the S^T layout.
 #pragma unroll
-    for (int i = 0; i < RPT; ++i)
+    for (int v = 0; v < 4; ++v) {
+      const float av = __shfl(alpha, 4 * q4 + v, 64);
 #pragma unroll
-      for (int w = 0; w < W; ++w)
+      for (int dt = 0; dt < DT; ++dt) acc[dt][v] *= av;
+    }
+    // P.V: k-step (tt, v) takes token tt * 16 + 4 q4 + v on lane quarter q4.
 #pragma unroll
-        for (int k = 0; k < 4; ++k) o[i][w][k] *= alpha[i];
-#pragma unroll 2
-    for (int t = 0; t < kPfChunk; t += 4) {
-      float4 v4[4][W];
+    for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int v = 0; v < 4; ++v) {
+        const float* vr = Vs + (tt * 16 + 4 * q4 + v) * KS + j16 * DT;
+        float vv[DT];
 #pragma unroll
-        for (int w = 0; w < W; ++w) v4[u][w] = *reinterpret_cast<const float4*>(Vs + (t + u) * HD + tg * 4 + 64 * w);
-#pragma unroll
-      for (int i = 0; i < RPT; ++i) {
-        const float4 p4 = *reinterpret_cast<const float4*>(Ps + (rg * RPT + i) * PS + t);
-#pragma unroll
-        for (int w = 0; w < W; ++w) {
-          fma4(o[i][w], p4.x, v4[0][w]);
-          fma4(o[i][w], p4.y, v4[1][w]);
-          fma4(o[i][w], p4.z, v4[2][w]);
-          fma4(o[i][w], p4.w, v4[3][w]);
+        for (int d4 = 0; d4 < DT; d4 += 4) {
+          const float4 x = *reinterpret_cast<const float4*>(vr + d4);
+          vv[d4] = x.x, vv[d4 + 1] = x.y, vv[d4 + 2] = x.z, vv[d4 + 3] = x.w;
         }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(st[tt][v], vv[dt], acc[dt], 0, 0, 0);
       }
-    }
-    __syncthreads();  // Ks / Vs / Ps are rewritten by the next chunk
+    __syncthreads();  // Ks / Vs are rewritten by the next chunk
   }
-
-  if constexpr (SHARED) {
+  // Row sums over the 4 lanes of each row, then moved to the output layout with the maxima.
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const int r = rg * RPT + i;
-      const int e = e0 + r / G;
-      if (e >= p.n || qpos[r / G] < 0) continue;
-      const int64_t ps = (static_cast<int64_t>(p.vmap[2 * e]) * p.heads + kvh * G + r % G) * p.nstride + p.vmap[2 * e + 1];
+  for (int v = 0; v < 4; ++v) {
+    const int orow = wave * 16 + 4 * q4 + v;
+    const float lv = __shfl(lsum, 4 * q4 + v, 64);
+    const float mv = __shfl(m, 4 * q4 + v, 64);
+    const int e = e0 + orow / G;
+    if (e >= p.n || qpos[orow / G] < 0) continue;
+    const int h = kvh * G + orow % G;
+    if constexpr (SHARED) {
+      const int64_t ps_ = (static_cast<int64_t>(p.vmap[2 * e]) * p.heads + h) * p.nstride + p.vmap[2 * e + 1];
 #pragma unroll
-      for (int w = 0; w < W; ++w)
-        *reinterpret_cast<float4*>(p.part_o + ps * HD + tg * 4 + 64 * w) =
-            make_float4(o[i][w][0], o[i][w][1], o[i][w][2], o[i][w][3]);
-      if (tg == 0) {
-        p.part_ml[2 * ps] = m[i];
-        p.part_ml[2 * ps + 1] = l[i];
+      for (int dt = 0; dt < DT; ++dt) p.part_o[ps_ * HD + j16 * DT + dt] = acc[dt][v];
+      if (j16 == 0) {
+        p.part_ml[2 * ps_] = mv;
+        p.part_ml[2 * ps_ + 1] = lv;
       }
-    }
-    return;
-  }
+    } else {
+      float* dst = p.out + static_cast<int64_t>(e) * p.ldo + h * HD + j16 * DT;
 #pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    const int r = rg * RPT + i;
-    const int e = e0 + r / G;
-    if (e >= p.n) continue;
-    float* dst = p.out + static_cast<int64_t>(e) * p.ldo + (kvh * G + r % G) * HD;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      float4 v;
-      v.x = l[i] > 0.0f ? o[i][w][0] / l[i] : 0.0f;
-      v.y = l[i] > 0.0f ? o[i][w][1] / l[i] : 0.0f;
-      v.z = l[i] > 0.0f ? o[i][w][2] / l[i] : 0.0f;
-      v.w = l[i] > 0.0f ? o[i][w][3] / l[i] : 0.0f;
-      *reinterpret_cast<float4*>(dst + tg * 4 + 64 * w) = v;
+      for (int dt = 0; dt < DT; ++dt) dst[dt] = lv > 0.0f ? acc[dt][v] / lv : 0.0f;
     }
   }
 }
 
 template <int HD>
-size_t pf_smem_bytes() {
-  constexpr int R = pf_rows<HD>();
-  constexpr int kPfChunk = pf_chunk<HD>();
-  return sizeof(float) * (R * (HD + kPfPad) + kPfChunk * (HD + kPfPad) + kPfChunk * HD + R * (kPfChunk + kPfPad)) +
-         sizeof(int) * (2 * kPfChunk + 2 * R);
+size_t rows_smem_bytes() {
+  constexpr int kRc = rows_chunk<HD>();
+  constexpr int QT = kRowsTile;  // upper bound (G = 1)
+  return sizeof(float) * (2 * kRc * (HD + kPfPad)) + sizeof(int) * (2 * kRc + 2 * QT);
 }
 
 template <int G, int HD, bool SHARED>
 void go_prefill(const PfParams& p, hipStream_t st) {
-  constexpr int QT = pf_rows<HD>() / G;
-  const size_t smem = pf_smem_bytes<HD>();
+  constexpr int QT = kRowsTile / G;
+  const size_t smem = rows_smem_bytes<HD>();
   static bool done = false;
   if (!done) {
     PIA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_prefill<G, HD, SHARED>),
@@ -803,7 +754,7 @@ AttnPlan plan_attention(int64_t n, int64_t num_kv_heads, int64_t head_dim, int64
   return plan;
 }
 
-int64_t attention_tile_rows() { return 32; }
+int64_t attention_tile_rows() { return kRowsTile; }
 
 int64_t attention_work_bytes(int64_t n, int64_t heads, int64_t head_dim, int64_t splits) {
   if (splits <= 1) return 0;
@@ -837,6 +788,7 @@ void launch_attention(const AttnLaunch& a, hipStream_t st) {
     PfParams pf{a.q,       a.ldq,  a.out, a.ldo, a.kv, a.layer * L.num_blocks * L.block_size, static_cast<int>(L.block_size),
                 static_cast<int>(L.num_kv_heads), static_cast<int>(a.heads), static_cast<int>(a.n),
                 1.0f / sqrtf(static_cast<float>(hd)), a.entries, a.tables};
+    pf.nstride = 1;
     if (hd == 64) prefill_by_g<64>(pf, g, st);
     else prefill_by_g<128>(pf, g, st);
     PIA_HIP(hipGetLastError());
