@@ -416,6 +416,8 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
   int* slots = reinterpret_cast<int*>(Vs + kRc * KS);  // [2][kRc]
   int* qpos = slots + 2 * kRc;         // [QT]
   int* qstart = qpos + QT;             // [QT]
+  int* mapped = qstart + QT;           // [2]: every token of the chunk is mapped
+  int64_t* rowoff = reinterpret_cast<int64_t*>(mapped + 2);  // [2][kRc]: float offset of the K row
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j16 = lane & 15, q4 = lane >> 4;
@@ -481,6 +483,8 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
     qv[m] = v.x, qv[m + 1] = v.y, qv[m + 2] = v.z, qv[m + 3] = v.w;
   }
 
+  const int64_t head_stride = 2 * static_cast<int64_t>(HD);
+  // Block ids of chunk c into dst, and into mapped[c & 1] whether every token of it is mapped.
   auto resolve = [&](int c, int* dst) {
     if (tid < kRc) {
       const int t = lo + c * kRc + tid;
@@ -490,30 +494,35 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
         if (lb < table_len) slot = p.tables[table_off + lb] * p.block_size + t % p.block_size;
       }
       dst[tid] = slot;
+      // Unmapped tokens read slot 0 of the layer (always inside the cache); zeroed in LDS.
+      rowoff[(c & 1) * kRc + tid] = ((p.layer_slots + max(slot, 0)) * p.hkv + kvh) * head_stride;
+      const unsigned long long unmapped = __ballot(slot < 0);
+      if (tid == 0) mapped[c & 1] = unmapped == 0;
     }
   };
-  const int64_t head_stride = 2 * static_cast<int64_t>(HD);
   // The loads stay raw in registers while in flight; unmapped tokens (which read slot 0 of the
   // layer, always inside the cache) are zeroed when the chunk is written to LDS.
   float4 kreg[KV4], vreg[KV4];
   bool kept[KV4];
-  auto load = [&](const int* sl) {
+  auto load = [&](int c) {
+    const int* sl = slots + (c & 1) * kRc;
+    const int64_t* ro = rowoff + (c & 1) * kRc;
 #pragma unroll
     for (int u = 0; u < KV4; ++u) {
       const int i = tid + u * kThreads;
       const int t = i / (HD / 4), d = (i % (HD / 4)) * 4;
-      const int slot = sl[t];
-      const float* src = p.kv + ((p.layer_slots + max(slot, 0)) * p.hkv + kvh) * head_stride + d;
+      const float* src = p.kv + ro[t] + d;
       kreg[u] = *reinterpret_cast<const float4*>(src);
       vreg[u] = *reinterpret_cast<const float4*>(src + HD);
-      kept[u] = slot >= 0;
+      kept[u] = sl[t] >= 0;
     }
   };
   auto zero_unless = [](bool keep, const float4& x) {
     return make_float4(keep ? x.x : 0.f, keep ? x.y : 0.f, keep ? x.z : 0.f, keep ? x.w : 0.f);
   };
 
-  float m = -INFINITY, lsum = 0.0f;  // this lane's row: running max, partial sum over its tokens
+  const float scale2 = p.scale * 1.44269504088896341f;  // softmax scale times log2(e)
+  float m = -INFINITY, lsum = 0.0f;  // this lane's row: running max (base 2), partial sum over its tokens
   f32x4 acc[DT];                     // O rows 4 * q4 + v, dims j16 * DT + dt
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -521,7 +530,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
   if (nchunks > 0) {
     resolve(0, slots);
     __syncthreads();
-    load(slots);
+    load(0);
   }
   for (int c = 0; c < nchunks; ++c) {
     const int* cur = slots + (c & 1) * kRc;
@@ -531,8 +540,13 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
     for (int u = 0; u < KV4; ++u) {
       const int i = tid + u * kThreads;
       const int t = i / (HD / 4), d = (i % (HD / 4)) * 4;
-      *reinterpret_cast<float4*>(Ks + t * KS + d) = zero_unless(kept[u], kreg[u]);
-      *reinterpret_cast<float4*>(Vs + t * KS + d) = zero_unless(kept[u], vreg[u]);
+      if (mapped[c & 1]) {
+        *reinterpret_cast<float4*>(Ks + t * KS + d) = kreg[u];
+        *reinterpret_cast<float4*>(Vs + t * KS + d) = vreg[u];
+      } else {
+        *reinterpret_cast<float4*>(Ks + t * KS + d) = zero_unless(kept[u], kreg[u]);
+        *reinterpret_cast<float4*>(Vs + t * KS + d) = zero_unless(kept[u], vreg[u]);
+      }
     }
     __syncthreads();
     if (c + 1 < nchunks) resolve(c + 1, nxt);
@@ -556,35 +570,50 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) st[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[tt].w, qv[m4 + 3], st[tt], 0, 0, 0);
     }
-    // Mask, scale, running max over the row (the 4 lanes j16 + 16 q share a row).
+    // Scale (base-2 logits: exp(x) = 2^(x log2 e)), mask, running max over the row (the 4
+    // lanes j16 + 16 q share a row). A chunk inside every window of the wave's rows, with all
+    // of its tokens mapped, needs no mask (the common case: all but the diagonal chunks).
+    const bool full = mapped[c & 1] && __all(c0 >= rstart && c0 + kRc - 1 <= rpos);
     float mx = -INFINITY;
+    if (full) {
 #pragma unroll
-    for (int tt = 0; tt < TT; ++tt)
+      for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int tk = tt * 16 + 4 * q4 + v;
-        const int t = c0 + tk;
-        const bool ok = cur[tk] >= 0 && t >= rstart && t <= rpos;
-        st[tt][v] = ok ? st[tt][v] * p.scale : -INFINITY;
-        mx = fmaxf(mx, st[tt][v]);
-      }
+        for (int v = 0; v < 4; ++v) {
+          st[tt][v] *= scale2;
+          mx = fmaxf(mx, st[tt][v]);
+        }
+    } else {
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int tk = tt * 16 + 4 * q4 + v;
+          const int t = c0 + tk;
+          const bool ok = cur[tk] >= 0 && t >= rstart && t <= rpos;
+          st[tt][v] = ok ? st[tt][v] * scale2 : -INFINITY;
+          mx = fmaxf(mx, st[tt][v]);
+        }
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m, mx);
-    const float alpha = (m == -INFINITY) ? 1.0f : expf(m - m_new);
+    const float alpha = (m == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
+    // A row with no visible token yet keeps m = -inf; its probabilities are 0.
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
     float ps = 0.0f;
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float pr = (m_new == -INFINITY) ? 0.0f : expf(st[tt][v] - m_new);
+        const float pr = __builtin_amdgcn_exp2f(st[tt][v] - m_use);
         st[tt][v] = pr;
         ps += pr;
       }
     lsum = __builtin_fmaf(lsum, alpha, ps);
     m = m_new;
     __syncthreads();  // every wave has read Ks; the next chunk's block ids are resolved
-    if (c + 1 < nchunks) load(nxt);
+    if (c + 1 < nchunks) load(c + 1);
     // Output rows 4 q4 + v take the factor of the lane that owns that row in the S^T layout.
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -625,7 +654,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) p.part_o[ps_ * HD + j16 * DT + dt] = acc[dt][v];
       if (j16 == 0) {
-        p.part_ml[2 * ps_] = mv;
+        p.part_ml[2 * ps_] = mv * 0.69314718055994531f;  // natural-log units, as k_attn writes
         p.part_ml[2 * ps_ + 1] = lv;
       }
     } else {
@@ -640,7 +669,7 @@ template <int HD>
 size_t rows_smem_bytes() {
   constexpr int kRc = rows_chunk<HD>();
   constexpr int QT = kRowsTile;  // upper bound (G = 1)
-  return sizeof(float) * (2 * kRc * (HD + kPfPad)) + sizeof(int) * (2 * kRc + 2 * QT);
+  return sizeof(float) * (2 * kRc * (HD + kPfPad)) + sizeof(int) * (2 * kRc + 2 * QT + 2) + sizeof(int64_t) * 2 * kRc;
 }
 
 template <int G, int HD, bool SHARED>
