@@ -413,11 +413,13 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
   float* Vs = Ks + kRc * KS;           // [kRc][KS]
   float* qstage = smem;                // [R][HD] query rows, before the first chunk only
   static_assert(2 * kRc * KS >= R * HD, "the query rows are staged where K/V go");
-  int* slots = reinterpret_cast<int*>(Vs + kRc * KS);  // [2][kRc]
-  int* qpos = slots + 2 * kRc;         // [QT]
+  // Per chunk c, in buffer c % 3 (resolved two chunks ahead): block ids, whether every token
+  // is mapped, and the float offset of each token's K row.
+  int* slots = reinterpret_cast<int*>(Vs + kRc * KS);  // [3][kRc]
+  int* qpos = slots + 3 * kRc;         // [QT]
   int* qstart = qpos + QT;             // [QT]
-  int* mapped = qstart + QT;           // [2]: every token of the chunk is mapped
-  int64_t* rowoff = reinterpret_cast<int64_t*>(mapped + 2);  // [2][kRc]: float offset of the K row
+  int* mapped = qstart + QT;           // [4]
+  int64_t* rowoff = reinterpret_cast<int64_t*>(mapped + 4);  // [3][kRc]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j16 = lane & 15, q4 = lane >> 4;
@@ -484,20 +486,20 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
   }
 
   const int64_t head_stride = 2 * static_cast<int64_t>(HD);
-  // Block ids of chunk c into dst, and into mapped[c & 1] whether every token of it is mapped.
-  auto resolve = [&](int c, int* dst) {
+  auto resolve = [&](int c) {
     if (tid < kRc) {
+      const int b = c % 3;
       const int t = lo + c * kRc + tid;
       int slot = -1;
       if (t <= hi) {
         const int lb = t / p.block_size;
         if (lb < table_len) slot = p.tables[table_off + lb] * p.block_size + t % p.block_size;
       }
-      dst[tid] = slot;
+      slots[b * kRc + tid] = slot;
       // Unmapped tokens read slot 0 of the layer (always inside the cache); zeroed in LDS.
-      rowoff[(c & 1) * kRc + tid] = ((p.layer_slots + max(slot, 0)) * p.hkv + kvh) * head_stride;
+      rowoff[b * kRc + tid] = ((p.layer_slots + max(slot, 0)) * p.hkv + kvh) * head_stride;
       const unsigned long long unmapped = __ballot(slot < 0);
-      if (tid == 0) mapped[c & 1] = unmapped == 0;
+      if (tid == 0) mapped[b] = unmapped == 0;
     }
   };
   // The loads stay raw in registers while in flight; unmapped tokens (which read slot 0 of the
@@ -505,8 +507,8 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
   float4 kreg[KV4], vreg[KV4];
   bool kept[KV4];
   auto load = [&](int c) {
-    const int* sl = slots + (c & 1) * kRc;
-    const int64_t* ro = rowoff + (c & 1) * kRc;
+    const int* sl = slots + (c % 3) * kRc;
+    const int64_t* ro = rowoff + (c % 3) * kRc;
 #pragma unroll
     for (int u = 0; u < KV4; ++u) {
       const int i = tid + u * kThreads;
@@ -528,19 +530,20 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (nchunks > 0) {
-    resolve(0, slots);
+    resolve(0);
+    if (nchunks > 1) resolve(1);
     __syncthreads();
     load(0);
   }
   for (int c = 0; c < nchunks; ++c) {
-    const int* cur = slots + (c & 1) * kRc;
-    int* nxt = slots + ((c + 1) & 1) * kRc;
+    const int* cur = slots + (c % 3) * kRc;
+    const bool cur_mapped = mapped[c % 3];
     const int c0 = lo + c * kRc;
 #pragma unroll
     for (int u = 0; u < KV4; ++u) {
       const int i = tid + u * kThreads;
       const int t = i / (HD / 4), d = (i % (HD / 4)) * 4;
-      if (mapped[c & 1]) {
+      if (cur_mapped) {
         *reinterpret_cast<float4*>(Ks + t * KS + d) = kreg[u];
         *reinterpret_cast<float4*>(Vs + t * KS + d) = vreg[u];
       } else {
@@ -549,7 +552,10 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
       }
     }
     __syncthreads();
-    if (c + 1 < nchunks) resolve(c + 1, nxt);
+    // Buffer (c + 2) % 3 was last read in chunk c - 1; chunk c + 1's ids were resolved before
+    // the last barrier, so its K/V loads go out now and are in flight for the whole chunk.
+    if (c + 2 < nchunks) resolve(c + 2);
+    if (c + 1 < nchunks) load(c + 1);
     // S^T tiles: token tt * 16 + 4 q4 + v, row j16 of this wave.
     // The TT tiles' dependency chains are interleaved so consecutive MFMAs are independent.
     f32x4 st[TT];
@@ -573,7 +579,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
     // Scale (base-2 logits: exp(x) = 2^(x log2 e)), mask, running max over the row (the 4
     // lanes j16 + 16 q share a row). A chunk inside every window of the wave's rows, with all
     // of its tokens mapped, needs no mask (the common case: all but the diagonal chunks).
-    const bool full = mapped[c & 1] && __all(c0 >= rstart && c0 + kRc - 1 <= rpos);
+    const bool full = cur_mapped && __all(c0 >= rstart && c0 + kRc - 1 <= rpos);
     float mx = -INFINITY;
     if (full) {
 #pragma unroll
@@ -612,8 +618,6 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
       }
     lsum = __builtin_fmaf(lsum, alpha, ps);
     m = m_new;
-    __syncthreads();  // every wave has read Ks; the next chunk's block ids are resolved
-    if (c + 1 < nchunks) load(c + 1);
     // Output rows 4 q4 + v take the factor of the lane that owns that row in the S^T layout.
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -669,7 +673,7 @@ template <int HD>
 size_t rows_smem_bytes() {
   constexpr int kRc = rows_chunk<HD>();
   constexpr int QT = kRowsTile;  // upper bound (G = 1)
-  return sizeof(float) * (2 * kRc * (HD + kPfPad)) + sizeof(int) * (2 * kRc + 2 * QT + 2) + sizeof(int64_t) * 2 * kRc;
+  return sizeof(float) * (2 * kRc * (HD + kPfPad)) + sizeof(int) * (3 * kRc + 2 * QT + 4) + sizeof(int64_t) * 3 * kRc;
 }
 
 template <int G, int HD, bool SHARED>
