@@ -588,152 +588,227 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 // the next stage's global loads are in registers while the current stage's MFMAs run. Four
 // waves, each 64 rows x 96 columns = 2 x 3 tiles of v_mfma_i32_32x32x32_i8.
 namespace tile {
-constexpr int kBM = 128, kBN = 192, kBK = 64;
-constexpr int kPitch = kBK;  // LDS row pitch in bytes; 16-byte chunks swizzled (dec::chunk_pos)
-constexpr int kStage = (kBM + kBN) * kPitch;
-constexpr int kWLoads = kBM * kBK / 16 / kThreads;  // 16-byte loads per thread per stage: 2
-constexpr int kDLoads = kBN * kBK / 16 / kThreads;  // 3
-constexpr size_t kSmem = 2 * kStage > 64 * kBN * 4 ? 2 * kStage : 64 * kBN * 4;
+// Tile: kBM = 32 TI WRW weight rows x kBN = 96 WCW digit rows (32 WCW batch entries), WRW x WCW
+// waves, each owning a 32 TI x 96 block of the result (TI x 3 MFMA 32x32 tiles); K stages of
+// kBK bytes in two LDS buffers, filled by direct global -> LDS loads one stage ahead. Where
+// the time goes (TinyLlama projections at 2048 tokens, 128 x 192 tile): the stage loop alone
+// (no operand loads, no epilogue) issues int8 MFMA at about 55% of the rate a pure MFMA loop
+// reaches; the operand loads add about half of that time again, the epilogue a sixth. Deeper
+// load pipelines (3 and 4 stages) measured no faster. The 256 x 384 tile (8 waves, 128 x 96
+// each) reads half the operand bytes per multiply-add; it is used when its grid still gives
+// every CU two workgroups (the gate/up projection of a long prefill).
+constexpr int kBK = 64;
+constexpr int kPitch = kBK;  // LDS row pitch in bytes
+// 16-byte chunk c of tile row n sits at position c ^ ((n >> 2) & 3). A 32x32x32 operand read
+// takes chunk kk / 16 + lane / 32 of rows lane % 32; the LDS serves 16 lanes of a 16-byte read
+// per cycle, and this swizzle puts the 16 rows of each such group on distinct banks (measured
+// with SQ_LDS_BANK_CONFLICT: 0 conflict cycles, against 4 per read with (n >> 1) & 3).
+__device__ inline int chunk_pos(int n, int c) { return (c ^ ((n >> 2) & 3)) * 16; }
+template <int TI, int WRW, int WCW>
+struct Shape {
+  static constexpr int kBM = 32 * TI * WRW, kBN = 96 * WCW, kWaves = WRW * WCW, kThreads = 64 * kWaves;
+  static constexpr int kStage = (kBM + kBN) * kPitch;
+  static constexpr size_t kSmem = 2 * kStage;
+};
+using Small = Shape<2, 2, 2>;  // 128 x 192, 4 waves
+using Big = Shape<4, 2, 4>;    // 256 x 384, 8 waves
 }  // namespace tile
 
-template <int EPI>
-__global__ __launch_bounds__(kThreads) void k_gemm_tile(const int8_t* __restrict__ W, int64_t ldw,
-                                                        const float* __restrict__ S, const int8_t* __restrict__ D,
-                                                        int kpad, int nrows, const float* __restrict__ pow2,
-                                                        float* __restrict__ O, int64_t osb, int64_t osr, int rows) {
+// Global -> LDS load of 16 bytes per lane with no register staging: lane l's bytes land at
+// LDS byte lds_base + 16 l (global_load_lds_dwordx4; M0 holds the wave-uniform LDS base and is
+// restored after). The compiler does not see the LDS write: callers order it with explicit
+// vmcnt waits and barriers (both also compiler memory barriers).
+__device__ __forceinline__ void load_lds16(const void* g, unsigned lds_base) {
+  unsigned saved;
+  // One wait state between the M0 write and the load that reads it.
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(g), "s"(lds_base)
+               : "memory");
+}
+__device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <int EPI, int TI, int WRW, int WCW>
+__global__ __launch_bounds__(64 * WRW * WCW, 2) void k_gemm_tile(const int8_t* __restrict__ W, int64_t ldw,
+                                                                 const float* __restrict__ S,
+                                                                 const int8_t* __restrict__ D, int kpad, int nrows,
+                                                                 const float* __restrict__ pow2, float* __restrict__ O,
+                                                                 int64_t osb, int64_t osr, int rows) {
   using namespace tile;
+  using Sh = Shape<TI, WRW, WCW>;
+  constexpr int kBM = Sh::kBM, kBN = Sh::kBN, kWaves = Sh::kWaves, kStage = Sh::kStage;
+  constexpr int kLoads = (kBM + kBN) / 16;  // direct loads per stage (16 rows each)
+  constexpr int kPerWave = (kLoads + kWaves - 1) / kWaves;
   extern __shared__ __align__(16) int8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row0 = blockIdx.x * kBM;
-  const int col0 = blockIdx.y * kBN;  // digit rows of D; batch entries 64 * blockIdx.y ..
-  const int wr = wave & 1, wc = wave >> 1;
+  const int col0 = blockIdx.y * kBN;  // digit rows of D; batch entries kBN / 3 * blockIdx.y ..
+  const int wr = wave % WRW, wc = wave / WRW;
   const int r_l = lane & 31, kh = lane >> 5;
 
-  // Global -> register staging of one K stage: thread t covers 16-byte segment (t % 4) of
-  // rows t / 4, t / 4 + 64, ... of each tile.
-  const int seg = tid & 3, trow = tid >> 2;
-  const int8_t* wsrc[kWLoads];
-  const int8_t* dsrc[kDLoads];
+  // Direct load L = wave + kWaves q fills rows 16 L .. + 16 of the stage (weights first, then
+  // digits); lane l writes LDS slot l % 4 of row 16 L + l / 4, which holds (swizzled) global
+  // chunk (l % 4) ^ ((row >> 2) & 3) of that row.
+  const int8_t* src[kPerWave];
+  bool digit[kPerWave];
 #pragma unroll
-  for (int u = 0; u < kWLoads; ++u)
-    wsrc[u] = W + static_cast<int64_t>(min(row0 + trow + 64 * u, rows - 1)) * ldw + seg * 16;
-#pragma unroll
-  for (int u = 0; u < kDLoads; ++u) dsrc[u] = D + static_cast<int64_t>(col0 + trow + 64 * u) * 64 + seg * 16;
-  v4i wreg[kWLoads], dreg[kDLoads];
-  auto gload = [&](int kt) {
+  for (int q = 0; q < kPerWave; ++q) {
+    const int n = 16 * min(wave + kWaves * q, kLoads - 1) + lane / 4;
+    digit[q] = n >= kBM;
+    src[q] = digit[q] ? D + static_cast<int64_t>(col0 + n - kBM) * 64 + chunk_pos(n, lane & 3)
+                      : W + static_cast<int64_t>(min(row0 + n, rows - 1)) * ldw + chunk_pos(n, lane & 3);
+  }
+  const unsigned lds0 = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds));
+  const int nk = kpad / kBK;
+  auto issue = [&](int kt, int b) {
     const int64_t off = static_cast<int64_t>(kt) * kBK;
     const int64_t doff = static_cast<int64_t>(kt) * nrows * 64;  // k-step-major digits
 #pragma unroll
-    for (int u = 0; u < kWLoads; ++u) wreg[u] = *reinterpret_cast<const v4i*>(wsrc[u] + off);
-#pragma unroll
-    for (int u = 0; u < kDLoads; ++u) dreg[u] = *reinterpret_cast<const v4i*>(dsrc[u] + doff);
-  };
-  auto sstore = [&](int buf) {
-    int8_t* ws = lds + buf * kStage;
-    int8_t* ds = ws + kBM * kPitch;
-#pragma unroll
-    for (int u = 0; u < kWLoads; ++u)
-      *reinterpret_cast<v4i*>(ws + (trow + 64 * u) * kPitch + dec::chunk_pos(trow + 64 * u, seg)) = wreg[u];
-#pragma unroll
-    for (int u = 0; u < kDLoads; ++u)
-      *reinterpret_cast<v4i*>(ds + (trow + 64 * u) * kPitch + dec::chunk_pos(trow + 64 * u, seg)) = dreg[u];
+    for (int q = 0; q < kPerWave; ++q)
+      if (wave + kWaves * q < kLoads)
+        load_lds16(src[q] + (digit[q] ? doff : off),
+                   __builtin_amdgcn_readfirstlane(lds0 + b * kStage + 16 * (wave + kWaves * q) * kPitch));
   };
 
-  v16i acc[2][3];
+  v16i acc[TI][3];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
     for (int j = 0; j < 3; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
-  const int nk = kpad / kBK;
-  gload(0);
-  sstore(0);
-  __syncthreads();
+  // Stage kt + 1 is in flight while stage kt is multiplied (more stages in flight measured no
+  // faster).
+  issue(0, 0);
   for (int kt = 0; kt < nk; ++kt) {
-    const bool more = kt + 1 < nk;
-    if (more) gload(kt + 1);
-    const int8_t* ws = lds + (kt & 1) * kStage;
+    const int b = kt & 1;
+    wait_vmcnt0();    // this wave's part of stage kt has landed
+    __syncthreads();  // ... every wave's; and buffer 1 - b (stage kt - 1) is free
+    if (kt + 1 < nk) issue(kt + 1, 1 - b);
+    const int8_t* ws = lds + b * kStage;
     const int8_t* ds = ws + kBM * kPitch;
 #pragma unroll
     for (int kk = 0; kk < kBK; kk += 32) {
-      v4i a[2], b[3];
+      v4i a[TI], bb[3];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        a[i] = *reinterpret_cast<const v4i*>(ws + (wr * 64 + i * 32 + r_l) * kPitch +
-                                             dec::chunk_pos(r_l, kk / 16 + kh));
+      for (int i = 0; i < TI; ++i)
+        a[i] = *reinterpret_cast<const v4i*>(ws + ((wr * TI + i) * 32 + r_l) * kPitch + chunk_pos(r_l, kk / 16 + kh));
 #pragma unroll
       for (int j = 0; j < 3; ++j)
-        b[j] = *reinterpret_cast<const v4i*>(ds + (wc * 96 + j * 32 + r_l) * kPitch +
-                                             dec::chunk_pos(r_l, kk / 16 + kh));
+        bb[j] = *reinterpret_cast<const v4i*>(ds + (wc * 96 + j * 32 + r_l) * kPitch + chunk_pos(r_l, kk / 16 + kh));
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 3; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 3; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bb[j], acc[i][j], 0, 0, 0);
     }
-    // Buffer (kt + 1) & 1 was last read in iteration kt - 1, before that iteration's barrier.
-    if (more) sstore((kt + 1) & 1);
-    __syncthreads();
   }
 
-  // Epilogue, 64 weight rows at a time: the C tile half goes to LDS ([64][kBN] int32), then
-  // thread -> (row, batch entry) recombines the entry's three digit columns. 32x32 result
-  // layout: lane holds column lane % 32 and, in register v, row 8 * (v / 4) + 4 * (lane / 32)
-  // + v % 4.
-  int* ct = reinterpret_cast<int*>(lds);
-  for (int half = 0; half < 2; ++half) {
-    if (wr == half) {
+  // Epilogue in registers. The three digit columns of a batch entry are 16 apart inside a
+  // 48-column group (digit_row), so in the 32x32 result layout (lane holds column lane % 32
+  // and, in register v, row 8 (v / 4) + 4 (lane / 32) + v % 4) one exchange between lanes l and
+  // l ^ 16 gives every lane the three digits of one entry: lanes c < 16 of the wave's columns
+  // take entry c (columns c, c + 16 of tile 0 and c of tile 1), lanes c >= 16 entry c
+  // (columns c of tile 1, c - 16 and c of tile 2). Each lane then owns 4 consecutive rows per
+  // register quad and writes them as one vector where the output layout allows.
+  const int e = wc * 32 + r_l;                  // entry of this lane within the tile
+  const int eg = col0 / 3 + e;                  // global batch entry
+  const bool lo = r_l < 16;
+  const float p2 = pow2[eg];
+  float* orow = O + static_cast<int64_t>(eg) * osb;
+  const bool vec = osr == 1 && (osb & 3) == 0;  // 16-byte aligned rows of 4 (8-byte pairs for SwiGLU)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TI; ++i) {
 #pragma unroll
-        for (int j = 0; j < 3; ++j)
+    for (int q = 0; q < 4; ++q) {
+      float y[4];
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int r = i * 32 + 8 * (v >> 2) + 4 * kh + (v & 3);
-            ct[r * kBN + wc * 96 + j * 32 + r_l] = acc[i][j][v];
-          }
-    }
-    __syncthreads();
-    const int b0 = col0 / 3;  // first batch entry of the tile
-    for (int idx = tid; idx < 64 * (kBN / 3); idx += kThreads) {
-      const int r = idx / (kBN / 3), b = idx % (kBN / 3);
-      const int row = row0 + half * 64 + r;
-      const int* cr = ct + r * kBN + digit_row(b, 0);  // digits j at cr[16 j]
-      const int64_t sum = static_cast<int64_t>(cr[0]) + 256 * static_cast<int64_t>(cr[16]) + 65536 * static_cast<int64_t>(cr[32]);
-      const float y = static_cast<float>(sum) * pow2[b0 + b];
+      for (int t = 0; t < 4; ++t) {
+        const int v = 4 * q + t;
+        const int x0 = acc[i][0][v], x1 = acc[i][1][v], x2 = acc[i][2][v];
+        const int sw = __shfl_xor(lo ? x2 : x0, 16, 64);
+        const int d0 = lo ? x0 : x1, d2 = lo ? x1 : x2;
+        const int64_t sum = static_cast<int64_t>(d0) + 256 * static_cast<int64_t>(sw) + 65536 * static_cast<int64_t>(d2);
+        y[t] = static_cast<float>(sum) * p2;
+      }
+      const int base = row0 + (wr * TI + i) * 32 + 8 * q + 4 * kh;  // rows base .. base + 3
       if constexpr (EPI == kEpiSwiglu) {
-        if ((r & 1) == 0 && row + 1 < rows) {
-          const int* cu = cr + kBN;
-          const int64_t su = static_cast<int64_t>(cu[0]) + 256 * static_cast<int64_t>(cu[16]) + 65536 * static_cast<int64_t>(cu[32]);
-          const float yu = static_cast<float>(su) * pow2[b0 + b];
-          const float g = y * S[row];
-          const float u = yu * S[row + 1];
-          const float silu = g / (1.0f + expf(-g));
-          O[static_cast<int64_t>(b0 + b) * osb + static_cast<int64_t>(row >> 1) * osr] = silu * u;
+        float o2[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int row = base + 2 * h;
+          const float g = y[2 * h] * S[min(row, rows - 1)];
+          const float u = y[2 * h + 1] * S[min(row + 1, rows - 1)];
+          o2[h] = g / (1.0f + expf(-g)) * u;
         }
-      } else if (row < rows) {
-        const float v = y * S[row];
-        float* o = O + static_cast<int64_t>(b0 + b) * osb + static_cast<int64_t>(row) * osr;
-        if (EPI == kEpiAdd) *o = *o + v;
-        else *o = v;
+        if (vec && base + 3 < rows) {
+          *reinterpret_cast<float2*>(orow + (base >> 1)) = make_float2(o2[0], o2[1]);
+        } else {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            if (base + 2 * h + 1 < rows) orow[static_cast<int64_t>((base >> 1) + h) * osr] = o2[h];
+        }
+      } else {
+        float o4[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o4[t] = y[t] * S[min(base + t, rows - 1)];
+        if (vec && base + 3 < rows) {
+          float4* dst = reinterpret_cast<float4*>(orow + base);
+          if constexpr (EPI == kEpiAdd) {
+            const float4 old = *dst;
+            *dst = make_float4(old.x + o4[0], old.y + o4[1], old.z + o4[2], old.w + o4[3]);
+          } else {
+            *dst = make_float4(o4[0], o4[1], o4[2], o4[3]);
+          }
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            if (base + t < rows) {
+              float* o = orow + static_cast<int64_t>(base + t) * osr;
+              if (EPI == kEpiAdd) *o = *o + o4[t];
+              else *o = o4[t];
+            }
+        }
       }
     }
-    __syncthreads();
   }
 }
 
-template <int EPI>
-void go_tile(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, int nrows, const float* pow2,
-             float* O, int64_t osb, int64_t osr, int rows, int tiles_n, hipStream_t st) {
+template <int EPI, int TI, int WRW, int WCW>
+void go_tile_shape(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, int nrows,
+                   const float* pow2, float* O, int64_t osb, int64_t osr, int rows, int tiles_n, hipStream_t st) {
+  using Sh = tile::Shape<TI, WRW, WCW>;
   static bool raised = false;
-  if (!raised && tile::kSmem > 65536) {
-    PIA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_tile<EPI>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(tile::kSmem)));
+  if (!raised && Sh::kSmem > 65536) {
+    PIA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_tile<EPI, TI, WRW, WCW>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(Sh::kSmem)));
     raised = true;
   }
-  hipLaunchKernelGGL((k_gemm_tile<EPI>), dim3((rows + tile::kBM - 1) / tile::kBM, tiles_n), dim3(kThreads), tile::kSmem,
-                     st, W, ldw, S, D, kpad, nrows, pow2, O, osb, osr, rows);
+  hipLaunchKernelGGL((k_gemm_tile<EPI, TI, WRW, WCW>), dim3((rows + Sh::kBM - 1) / Sh::kBM, tiles_n),
+                     dim3(Sh::kThreads), Sh::kSmem, st, W, ldw, S, D, kpad, nrows, pow2, O, osb, osr, rows);
+}
+
+// `chunks` whole 64-entry chunks of digits from D (pow2 and O at the same first entry): the
+// 256 x 384 tile over pairs of chunks when its grid gives every CU at least two workgroups,
+// the 128 x 192 tile otherwise and for an odd last chunk.
+template <int EPI>
+void go_tile(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int kpad, int nrows, const float* pow2,
+             float* O, int64_t osb, int64_t osr, int rows, int chunks, hipStream_t st) {
+  int dev = 0, cus = 0;
+  PIA_HIP(hipGetDevice(&dev));
+  PIA_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  const int64_t big_grid = static_cast<int64_t>((rows + tile::Big::kBM - 1) / tile::Big::kBM) * (chunks / 2);
+  const bool big = big_grid >= 2 * cus;
+  int done = 0;
+  if (big) {
+    go_tile_shape<EPI, 4, 2, 4>(W, ldw, S, D, kpad, nrows, pow2, O, osb, osr, rows, chunks / 2, st);
+    done = chunks / 2 * 2;
+  }
+  if (done < chunks) {
+    const int64_t b0 = 64 * static_cast<int64_t>(done);
+    go_tile_shape<EPI, 2, 2, 2>(W, ldw, S, D + 3 * b0 * 64, kpad, nrows, pow2 + b0, O + b0 * osb, osb, osr, rows,
+                                chunks - done, st);
+  }
 }
 
 }  // namespace
