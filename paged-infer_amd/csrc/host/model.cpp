@@ -429,6 +429,7 @@ struct pia_model {
   // the winning row) and wait for the step.
   void read_argmax(int32_t* out, int64_t batch, bool step = false) {
     const size_t bytes = batch * kArgmaxSlots * 8;
+    PIA_REQUIRE(bytes <= amax.bytes, "argmax read-back larger than the argmax slots");
     pin_out.ensure(bytes + 64);
     PIA_HIP(hipMemcpyAsync(pin_out.ptr, amax.ptr, bytes, hipMemcpyDeviceToHost, st()));
     int* err_h = reinterpret_cast<int*>(static_cast<char*>(pin_out.ptr) + bytes);
@@ -965,8 +966,10 @@ pia_model::StepDev upload_decode_step(pia_model* m, const std::vector<int32_t>& 
         m->tab_mirror[b * tc + i] = id;
       }
     PIA_HIP(hipMemcpyAsync(d, p, off_t, hipMemcpyHostToDevice, m->st()));
+    PIA_REQUIRE(tab_bytes <= m->tab_dev.bytes && off_t + tab_bytes <= m->pin.bytes, "block-table image exceeds its buffers");
     PIA_HIP(hipMemcpyAsync(m->tab_dev.ptr, img, tab_bytes, hipMemcpyHostToDevice, m->st()));
   } else {
+    PIA_REQUIRE(off_t + tab_bytes <= m->pin.bytes && off_t + tab_bytes <= m->step.bytes, "table patch exceeds the staging buffers");
     if (!patch.empty()) std::memcpy(p + off_t, patch.data(), tab_bytes);
     PIA_HIP(hipMemcpyAsync(d, p, off_t + tab_bytes, hipMemcpyHostToDevice, m->st()));
     launch_table_patch(m->tab_dev.as<int32_t>(), reinterpret_cast<const int32_t*>(d + off_t),
@@ -1156,6 +1159,7 @@ pia_status pia_model_decode(pia_model* m, const uint32_t* tokens, const int64_t*
     });
   }
   if (logits)
+    PIA_REQUIRE(static_cast<size_t>(batch * m->ld_v * 4) <= m->logits.bytes, "logits read-back exceeds the logits buffer");
     PIA_HIP(hipMemcpy2DAsync(logits, c.vocab * 4, m->logits.ptr, m->ld_v * 4, c.vocab * 4, batch,
                              hipMemcpyDeviceToHost, m->st()));
   m->last_path = step ? 1 : 0;
