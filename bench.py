@@ -116,6 +116,24 @@ def run_b1(ctx, cfg, weights, steps, warmup, prompt_len=512):
     for cls in ("qkv", "o", "gate_up", "down", "lm_head"):
         us, by = model.bench_class(cls, 1)
         prof["launch"][cls] = {"us": round(us, 3), "bytes": by, "GB/s": round(by / us / 1e3, 1)}
+    # Per-class time of a step from graph replays: each projection class's launches (above)
+    # times its launches per step; attention and the small kernels are what is left of the
+    # timed step.
+    ms_step = 1e3 * elapsed / steps
+    layers = cfg.layers
+    gb = {cls: round(prof["launch"][cls]["us"] * (1 if cls == "lm_head" else layers) / 1e3, 4)
+          for cls in ("qkv", "o", "gate_up", "down", "lm_head")}
+    gb["attention_and_rest"] = round(ms_step - sum(gb.values()), 4)
+    prof["graph_breakdown"] = gb
+    # Whole-step HBM rate: every weight byte and the KV bytes attention reads, per timed step.
+    step_bytes = model.weight_bytes() + prof["attn_bytes"]
+    prof["step_hbm"] = {"bytes_per_step": int(step_bytes), "GB/s": round(step_bytes / ms_step / 1e6, 1),
+                        "frac": round(step_bytes / ms_step / 1e6 / HBM_PEAK_GBS, 4)}
+    # The Llama-3-8B LM head (128256 x 4096 int8, 525 MB) at batch 1: the largest single GEMV
+    # of the configurations, long enough to show the kernel's streaming rate.
+    us, by = pia.bench_projection(ctx, 128256, 4096, 1, 10)
+    prof["big_gemv"] = {"rows": 128256, "cols": 4096, "us": round(us, 2), "bytes": by, "GB/s": round(by / us / 1e3, 1),
+                        "frac": round(by / us / 1e3 / HBM_PEAK_GBS, 4)}
     res = dict(tok_s=steps / elapsed, ms_per_step=1e3 * elapsed / steps, prefill_tok_s=prompt_len / prefill_s,
                last_tok=toks[0], last_pos=pos[0], table=table, nb=nb, weight_bytes=model.weight_bytes(), **prof)
     model.close()
@@ -555,7 +573,12 @@ def main():
                      "timing": "HIP events around a graph replay of the 22 gate/up launches of a step "
                                "(model weights, fused RMSNorm + SwiGLU), on the library stream"},
         "projections_b1": b1["launch"],
-        "step_breakdown_ms": {k: round(v["ms_per_step"], 4) for k, v in b1["classes"].items()},
+        # Eager pass, one event pair per launch: overstates every class a little (the events
+        # and the device spin are not free); the graph-replay figures below sum to the step.
+        "step_breakdown_eager_ms": {k: round(v["ms_per_step"], 4) for k, v in b1["classes"].items()},
+        "step_breakdown_graph_ms": b1["graph_breakdown"],
+        "step_hbm": b1["step_hbm"],
+        "lm_head_llama3_b1": b1["big_gemv"],
     }
     if cpu:
         log("CPU baseline (batch 1)")

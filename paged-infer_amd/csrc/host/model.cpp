@@ -1158,10 +1158,11 @@ pia_status pia_model_decode(pia_model* m, const uint32_t* tokens, const int64_t*
                      Epi::Store, m->amax.as<unsigned long long>());
     });
   }
-  if (logits)
+  if (logits) {
     PIA_REQUIRE(static_cast<size_t>(batch * m->ld_v * 4) <= m->logits.bytes, "logits read-back exceeds the logits buffer");
     PIA_HIP(hipMemcpy2DAsync(logits, c.vocab * 4, m->logits.ptr, m->ld_v * 4, c.vocab * 4, batch,
                              hipMemcpyDeviceToHost, m->st()));
+  }
   m->last_path = step ? 1 : 0;
   m->logit_rows = batch;
   m->read_argmax(argmax, batch, step);
