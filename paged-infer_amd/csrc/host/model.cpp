@@ -94,9 +94,6 @@ struct pia_model {
 
   int64_t cap = 0;  // rows of activation scratch
   DeviceBuffer x, xb, qkv, attn, h, logits, amax, attn_work, step, xq;
-  // Attention split arrival counters, one per (entry, kv head): zero between launches (the
-  // kernel that merges the splits re-arms them), zeroed here when (re)allocated.
-  DeviceBuffer attn_cnt;
   DeviceBuffer dec_split;  // split-K partial sums and counters of the decode GEMM
   bool dec_split_on = true;
   int64_t mfma_min = kMfmaMinBatch;
@@ -143,13 +140,6 @@ struct pia_model {
     PIA_HIP(hipStreamSynchronize(st()));
     drop_graphs();
     b.ensure(need);
-  }
-
-  void ensure_counters(int64_t n) {
-    const size_t need = static_cast<size_t>(n * cfg.kv_heads) * sizeof(unsigned);
-    if (need <= attn_cnt.bytes) return;
-    grow(attn_cnt, need);
-    PIA_HIP(hipMemset(attn_cnt.ptr, 0, attn_cnt.bytes));
   }
 
   void begin(int cls, int64_t bytes, hipEvent_t* b) {
@@ -320,8 +310,7 @@ struct pia_model {
                                kv.as<float>(), layout, c.heads, n, l, st());
         AttnLaunch a{QKV, ld_qkv, ATT, ld_h, kv.as<float>(), &layout, c.heads, in.entries, in.tables, n, l, plan,
                      attn_work.ptr, fused, rope_cos.as<float>(), rope_sin.as<float>(), prefill,
-                     in.shared_entries, in.shared_vmap, in.n_shared, in.shared_splits,
-                     attn_cnt.as<unsigned>()};
+                     in.shared_entries, in.shared_vmap, in.n_shared, in.shared_splits};
         launch_attention(a, st());
       });
       gemv(L.o, ATT, ld_h, nullptr, X, ld_h, n, Epi::Add);
@@ -1142,7 +1131,6 @@ pia_status pia_model_decode(pia_model* m, const uint32_t* tokens, const int64_t*
   m->grow(m->logits, batch * m->ld_v * 4);
   const int64_t wb = attention_work_bytes(batch, c.heads, m->hd, plan.splits + (shared ? sh.splits : 0));
   if (wb) m->grow(m->attn_work, wb);
-  m->ensure_counters(batch);
   const bool step = batch == 1 && m->step_ready() &&
                     max_window <= m->step_shape.max_splits * m->step_shape.max_tokens;
   const pia_model::StepDev in = upload_decode_step(m, tok, ent, tables, shared ? &sh : nullptr);
@@ -1201,7 +1189,6 @@ pia_status pia_model_prefill(pia_model* m, const uint32_t* tokens, int64_t n, in
   m->grow(m->logits, m->ld_v * 4);
   const int64_t wb = attention_work_bytes(n, c.heads, m->hd, plan.splits);
   if (wb) m->grow(m->attn_work, wb);
-  m->ensure_counters(n);
   const pia_model::StepDev in = upload_step(m, tok, ent, table, table_len);
   m->run_step({1, n, plan.split, plan.splits, plan.chunk, fused ? 1 : 0, 0, 0}, false, [&] {
     m->run_layers(n, in, plan, fused, mapped, true);

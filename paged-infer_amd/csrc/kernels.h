@@ -140,9 +140,6 @@ struct AttnLaunch {
   const pia_attn_entry* shared_entries = nullptr;
   const int32_t* shared_vmap = nullptr;  // [n_shared][2]: real entry, split slot
   int64_t n_shared = 0, shared_splits = 0;
-  // n x num_kv_heads arrival counters, zero on entry and left zero: with them the last split
-  // of each (entry, kv head) merges the splits; without, a combine kernel follows.
-  unsigned* counters = nullptr;
 };
 // Query rows (positions x heads of one kv head) per tile of the shared-prefix / prefill kernel.
 int64_t attention_tile_rows();

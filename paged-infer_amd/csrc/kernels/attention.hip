@@ -55,9 +55,6 @@ struct AttnParams {
   float* part_ml;
   const float* rope_cos;
   const float* rope_sin;
-  // Per (entry, kv head) arrival counters (zero between launches) when the last split to
-  // finish merges the splits itself; null: k_attn_combine runs after the launch.
-  unsigned* cnt;
 };
 
 // HD: compile-time head_dim (0 = runtime p.hd, for unusual shapes); every loop over the head
@@ -134,25 +131,6 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnParams p) {
   float o[G][4];
 #pragma unroll
   for (int g = 0; g < G; ++g) o[g][0] = o[g][1] = o[g][2] = o[g][3] = 0.0f;
-  // V rows of a chunk: hd/4 threads per token group, 4 consecutive dims each, kVT tokens per
-  // thread per pass (with a compile-time head_dim every token of the chunk a thread owns is in
-  // one pass, up to 16; otherwise 4 at a time). Unmapped and out-of-chunk tokens load nothing.
-  constexpr int kVTfull = HD ? kChunk / (kThreads / (HD ? HD / 4 : 1)) : 4;
-  constexpr int kVT = kVTfull < 16 ? kVTfull : 16;
-  auto load_v = [&](int c0, int count, int i0, float4 (&v4)[kVT], int (&idx)[kVT]) {
-#pragma unroll
-    for (int u = 0; u < kVT; ++u) {
-      const int i = i0 + u * ngrp;
-      const int slot = i < count ? slot_of[i] : -1;
-      idx[u] = slot >= 0 ? i : -1;
-      if (slot >= 0) {
-        const float* vp = (FUSED && own && c0 + i == en.pos) ? vnew : kv_at(slot) + hd;
-        v4[u] = *reinterpret_cast<const float4*>(vp + d4);
-      } else {
-        v4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
-  };
 
   for (int c0 = t0; c0 < t1; c0 += kChunk) {
     const int count = min(kChunk, t1 - c0);
@@ -246,17 +224,32 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnParams p) {
     }
     __syncthreads();
 
-    // V accumulation.
+    // V accumulation: hd/4 threads per token group, 4 consecutive dims each. With a
+    // compile-time head_dim every token of the chunk a thread owns is loaded before the first
+    // FMA (kChunk / ngrp loads in flight); otherwise 4 at a time.
     if (grp < ngrp) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const float alpha = stat[4 * g + 2];
         o[g][0] *= alpha, o[g][1] *= alpha, o[g][2] *= alpha, o[g][3] *= alpha;
       }
+      constexpr int kVTfull = HD ? kChunk / (kThreads / (HD ? HD / 4 : 1)) : 4;
+      constexpr int kVT = kVTfull < 16 ? kVTfull : 16;  // tokens per thread per pass
       for (int i0 = grp; i0 < count; i0 += kVT * ngrp) {
         float4 v4[kVT];
         int idx[kVT];
-        load_v(c0, count, i0, v4, idx);
+#pragma unroll
+        for (int u = 0; u < kVT; ++u) {
+          const int i = i0 + u * ngrp;
+          const int slot = i < count ? slot_of[i] : -1;
+          idx[u] = slot >= 0 ? i : -1;
+          if (slot >= 0) {
+            const float* vp = (FUSED && own && c0 + i == en.pos) ? vnew : kv_at(slot) + hd;
+            v4[u] = *reinterpret_cast<const float4*>(vp + d4);
+          } else {
+            v4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+        }
 #pragma unroll
         for (int u = 0; u < kVT; ++u) {
           if (idx[u] < 0) continue;
@@ -291,70 +284,12 @@ __global__ __launch_bounds__(kThreads) void k_attn(AttnParams p) {
       p.out[static_cast<int64_t>(e) * p.ldo + h * hd + d] = l > 0.0f ? acc / l : 0.0f;
     } else {
       const int64_t ps = (static_cast<int64_t>(e) * p.heads + h) * p.nstride + p.split_base + s;
-      if (p.cnt) {
-        // Agent-scope stores: they reach the point of coherence for every XCD's L2 without a
-        // cache writeback, so completing them (below) orders them before the arrival count.
-        __hip_atomic_store(p.part_o + ps * hd + d, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (d == 0) {
-          __hip_atomic_store(p.part_ml + 2 * ps, stat[4 * g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(p.part_ml + 2 * ps + 1, stat[4 * g + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      } else {
-        p.part_o[ps * hd + d] = acc;
-        if (d == 0) {
-          p.part_ml[2 * ps] = stat[4 * g];
-          p.part_ml[2 * ps + 1] = stat[4 * g + 1];
-        }
+      p.part_o[ps * hd + d] = acc;
+      if (d == 0) {
+        p.part_ml[2 * ps] = stat[4 * g];
+        p.part_ml[2 * ps + 1] = stat[4 * g + 1];
       }
     }
-  }
-  if (p.nstride == 1 || !p.cnt) return;
-  // The last of the nsplit workgroups of this (entry, kv head) to arrive merges all nstride
-  // partials of its G heads (log-sum-exp, as k_attn_combine) with agent-scope loads, and
-  // re-arms the counter. (The shared-prefix slots below split_base were written by an earlier
-  // launch.)
-  __shared__ int is_last;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (tid == 0) {
-    unsigned* c = p.cnt + static_cast<int64_t>(e) * p.hkv + kvh;
-    const unsigned prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = prev + 1 == static_cast<unsigned>(p.nsplit);
-    if (is_last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!is_last) return;
-  auto ld = [](const float* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
-  float* wgt = sc;  // [G][nstride] split weights (nstride <= kChunk)
-  for (int i = tid; i < G * p.nstride; i += kThreads) {
-    const int g = i / p.nstride, k = i % p.nstride;
-    const int64_t base = (static_cast<int64_t>(e) * p.heads + kvh * G + g) * p.nstride;
-    wgt[i] = ld(p.part_ml + 2 * (base + k));
-  }
-  __syncthreads();
-  if (tid < G) {  // per head: maximum, weights exp(m_k - M), and the total sum
-    const int g = tid;
-    const int64_t base = (static_cast<int64_t>(e) * p.heads + kvh * G + g) * p.nstride;
-    float mx = -INFINITY;
-    for (int k = 0; k < p.nstride; ++k) mx = fmaxf(mx, wgt[g * p.nstride + k]);
-    float l = 0.0f;
-    for (int k = 0; k < p.nstride; ++k) {
-      const float mk = wgt[g * p.nstride + k];
-      const float wk = (mx == -INFINITY || mk == -INFINITY) ? 0.0f : expf(mk - mx);
-      wgt[g * p.nstride + k] = wk;
-      l = __builtin_fmaf(ld(p.part_ml + 2 * (base + k) + 1), wk, l);
-    }
-    stat[4 * g + 1] = l;
-  }
-  __syncthreads();
-  for (int idx = tid; idx < G * hd; idx += kThreads) {
-    const int g = idx / hd, d = idx % hd;
-    const int h = kvh * G + g;
-    const int64_t base = (static_cast<int64_t>(e) * p.heads + h) * p.nstride;
-    float acc = 0.0f;
-    for (int k = 0; k < p.nstride; ++k) acc = __builtin_fmaf(ld(p.part_o + (base + k) * hd + d), wgt[g * p.nstride + k], acc);
-    const float l = stat[4 * g + 1];
-    p.out[static_cast<int64_t>(e) * p.ldo + h * hd + d] = l > 0.0f ? acc / l : 0.0f;
   }
 }
 
@@ -926,7 +861,6 @@ void launch_attention(const AttnLaunch& a, hipStream_t st) {
   }
   p.rope_cos = a.rope_cos;
   p.rope_sin = a.rope_sin;
-  p.cnt = p.nstride <= a.plan.chunk ? a.counters : nullptr;  // the merge's weights live in the score tile
   dim3 grid(static_cast<unsigned>(a.plan.splits), static_cast<unsigned>(L.num_kv_heads), static_cast<unsigned>(a.n));
   const size_t smem = attn_smem_bytes(g, hd, static_cast<int>(a.plan.chunk));
   switch (g) {
@@ -938,7 +872,7 @@ void launch_attention(const AttnLaunch& a, hipStream_t st) {
     default: fail(PIA_ERR_INVALID, "attention: kv_group must be 1, 2, 4, 8 or 16");
   }
   PIA_HIP(hipGetLastError());
-  if (p.nstride > 1 && !p.cnt) {
+  if (p.nstride > 1) {
     hipLaunchKernelGGL(k_attn_combine, dim3(static_cast<unsigned>(a.n * a.heads)), dim3(kMaxHd), 0, st, p.part_o,
                        p.part_ml, a.out, a.ldo, static_cast<int>(a.heads), hd, p.nstride);
     PIA_HIP(hipGetLastError());
