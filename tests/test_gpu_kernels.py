@@ -28,7 +28,11 @@ def _proj_bound(q, s, x):
 SHAPES = [(1, 1, 1), (3, 7, 2), (17, 33, 3), (344, 128, 1), (128, 344, 5), (64, 129, 8), (2560, 2048, 1),
           (2048, 5632, 1), (11264, 2048, 2), (1000, 2048, 13), (333, 4096, 32), (32000, 2048, 1),
           # small batches on the LDS-staged kernel, including row groups split by LDS capacity
-          (11264, 2048, 5), (2048, 5632, 6), (4096, 14336, 3), (50, 64, 16), (64, 48, 9), (2560, 2048, 8)]
+          (11264, 2048, 5), (2048, 5632, 6), (4096, 14336, 3), (50, 64, 16), (64, 48, 9), (2560, 2048, 8),
+          # prefill tiles: 128 x 192 with a ragged tail; 256 x 384 over pairs of 64-entry chunks, the
+          # odd last chunk on a 128 x 192 tile and a ragged tail (the [row][batch] output takes the
+          # strided epilogue stores, the [batch][row] one the vector stores)
+          (2560, 384, 300), (16384, 256, 1027)]
 
 
 @pytest.mark.parametrize("rows,cols,batch", SHAPES)
