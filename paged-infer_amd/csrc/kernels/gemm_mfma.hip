@@ -583,10 +583,9 @@ void go_dec(const int8_t* W, int64_t ldw, const float* S, const int8_t* D, int k
 
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-// Prefill GEMM (many batch entries): one workgroup per 128 weight rows x 192 digit columns
-// (64 batch entries). Both operand tiles go through LDS in 64-byte K stages, double buffered:
-// the next stage's global loads are in registers while the current stage's MFMAs run. Four
-// waves, each 64 rows x 96 columns = 2 x 3 tiles of v_mfma_i32_32x32x32_i8.
+// Prefill GEMM (many batch entries): workgroup tiles of weight rows x digit columns whose
+// operand stages go straight from memory to LDS, each wave multiplying its block of the tile
+// with v_mfma_i32_32x32x32_i8 (shapes and measurements below).
 namespace tile {
 // Tile: kBM = 32 TI WRW weight rows x kBN = 96 WCW digit rows (32 WCW batch entries), WRW x WCW
 // waves, each owning a 32 TI x 96 block of the result (TI x 3 MFMA 32x32 tiles); K stages of
@@ -610,8 +609,7 @@ struct Shape {
   static constexpr int kStage = (kBM + kBN) * kPitch;
   static constexpr size_t kSmem = 2 * kStage;
 };
-using Small = Shape<2, 2, 2>;  // 128 x 192, 4 waves
-using Big = Shape<4, 2, 4>;    // 256 x 384, 8 waves
+using Big = Shape<4, 2, 4>;  // 256 x 384, 8 waves (the other shape: Shape<2, 2, 2>, 128 x 192, 4 waves)
 }  // namespace tile
 
 // Global -> LDS load of 16 bytes per lane with no register staging: lane l's bytes land at
