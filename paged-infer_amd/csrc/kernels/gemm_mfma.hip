@@ -142,11 +142,11 @@ __global__ __launch_bounds__(kThreads) void k_xdigits(const float* __restrict__ 
   if (threadIdx.x == 0) pow2[b] = ldexpf(1.0f, -sh);
 }
 
-// The same digits with one wavefront per activation row (four rows per workgroup): shuffle
-// reductions only, 16-byte loads, four digits per 32-bit store. For rows of up to
-// 64 * 4 * kV4 <= 8192 floats with cols % 4 == 0 and 16-byte aligned rows; the row is held
-// in registers between the reductions and the digit split. Longer rows keep one workgroup
-// per row (k_xdigits), which spreads them over more lanes.
+// The same digits with W wavefronts per activation row (4 / W rows per workgroup; the launch
+// uses W = 4): shuffle reductions (and the W partials through LDS), 16-byte loads, four digits
+// per 32-bit store. For rows of up to 64 * W * kV4 floats with cols % 4 == 0 and 16-byte
+// aligned rows; the row is held in registers between the reductions and the digit split.
+// Longer rows use k_xdigits.
 template <int kV4, int W>
 __global__ __launch_bounds__(256) void k_xdigits_wave(const float* __restrict__ x, int64_t ldx,
                                                       const float* __restrict__ nw, float eps, int cols, int batch,
