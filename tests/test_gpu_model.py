@@ -151,15 +151,15 @@ PREFILL_ATTN = [  # hidden, heads, kv_heads, window, prompt tokens, resume split
     (256, 4, 4, 45, 130, 0),      # one head per kv head, sliding window of 45
     (512, 4, 2, None, 100, 0),    # head_dim 128
     (1024, 8, 4, 70, 160, 64),    # head_dim 128, window, resumed prefill
-    (1024, 16, 1, None, 150, 0),  # head_dim 64, 16 heads per kv head (two positions per tile)
+    (1024, 16, 1, None, 150, 0),  # head_dim 64, 16 heads per kv head (four positions per tile)
 ]
 
 
 @pytest.mark.parametrize("case", range(len(PREFILL_ATTN)))
 def test_prefill_tiled_attention(ctx, case):
-    """Prefills of 64 or more positions run the query-tiled attention kernel (32 query-head
-    rows per workgroup: 32/G positions x the G heads of a kv head; K/V staged in LDS by 64-token
-    chunks, 32 at head_dim 128). Logits of the last position and the K/V written by the prefill (through
+    """Prefills of 64 or more positions run the query-tiled attention kernel (64 query-head
+    rows per workgroup: 64/G positions x the G heads of a kv head, causal tiles paired; K/V
+    staged in LDS by 64-token chunks, 32 at head_dim 128). Logits of the last position and the K/V written by the prefill (through
     the greedy decode steps that follow) are compared with the oracle."""
     hidden, heads, kvh, window, n, split = PREFILL_ATTN[case]
     print(f"[prefill-attn] hidden={hidden} heads={heads} kv={kvh} window={window} n={n} split={split}", flush=True)
