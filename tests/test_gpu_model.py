@@ -155,6 +155,15 @@ PREFILL_ATTN = [  # hidden, heads, kv_heads, window, prompt tokens, resume split
 ]
 
 
+@pytest.mark.parametrize("case", [0, 2, 4])
+def test_prefill_tiled_attention_paired(ctx, case, monkeypatch):
+    """The causal tile pairing (a workgroup takes tiles t and n - 1 - t) runs by default only on
+    grids large enough to fill the chip when halved; here it is forced on small
+    prefills: an even tile count, an odd one (the middle tile alone) and a resumed prefill."""
+    monkeypatch.setenv("PIA_PREFILL_PAIR", "1")
+    test_prefill_tiled_attention(ctx, case)
+
+
 @pytest.mark.parametrize("case", range(len(PREFILL_ATTN)))
 def test_prefill_tiled_attention(ctx, case):
     """Prefills of 64 or more positions run the query-tiled attention kernel (64 query-head
